@@ -1,0 +1,166 @@
+// Shared device helpers for the MoE kernels: number formats, wave64 reductions and the CDNA4 MFMA
+// fragments every grouped product uses. gfx950 only.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/flide_moe.h"
+
+typedef uint16_t u16;
+typedef uint8_t u8;
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef int i32x8_t __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+#define FLIDE_DEV __device__ __forceinline__
+
+// ---------------------------------------------------------------------------------------------------
+// number formats
+// ---------------------------------------------------------------------------------------------------
+FLIDE_DEV float bf16_to_f32(u16 v) { return __uint_as_float((uint32_t)v << 16); }
+
+// float32 -> bfloat16 bits, round to nearest even; NaN stays a (quiet) NaN.
+FLIDE_DEV u16 f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u16)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (u16)(u >> 16);
+}
+
+FLIDE_DEV float f16_to_f32(u16 v) { return (float)__builtin_bit_cast(_Float16, v); }
+FLIDE_DEV u16 f32_to_f16(float f) { return __builtin_bit_cast(u16, (_Float16)f); }
+
+FLIDE_DEV float bf16_round(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+
+// float32 with |x| <= 448 -> OCP e4m3fn byte (S EEEE MMM, bias 7), round to nearest even. Normal
+// numbers keep 3 mantissa bits; below 2^-6 the quantum is 2^-9 (subnormals). Inputs above 448 in
+// magnitude saturate to 448 (callers clamp first, as flide/kernels/fp8.py:42 does).
+FLIDE_DEV u8 f32_to_e4m3fn(float x) {
+  uint32_t u = __float_as_uint(x);
+  uint32_t sign = (u >> 24) & 0x80u;
+  uint32_t a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return (u8)(sign | 0x7fu);           // NaN
+  if (a >= 0x43e00000u) return (u8)(sign | 0x7eu);          // >= 448: saturate
+  int e = (int)(a >> 23) - 127;                             // unbiased exponent of |x|
+  if (e < -6) {
+    // subnormal range of e4m3fn: value = m * 2^-9, m in [0, 8]; 8 means the smallest normal 2^-6
+    float q = __uint_as_float(a) * 512.0f;                  // exact scaling by 2^9
+    float r = __builtin_rintf(q);                           // ties to even (default rounding mode)
+    uint32_t m = (uint32_t)r;
+    return (u8)(sign | m);                                  // m == 8 encodes exponent field 1, mantissa 0
+  }
+  // normal: keep 3 mantissa bits of the float32 mantissa with round to nearest even
+  uint32_t mant = a & 0x7fffffu;
+  uint32_t lsb = (mant >> 20) & 1u;
+  uint32_t rounded = a + 0x7ffffu + lsb;                    // may carry into the exponent
+  int e2 = (int)(rounded >> 23) - 127;
+  uint32_t m3 = (rounded >> 20) & 7u;
+  uint32_t code = ((uint32_t)(e2 + 7) << 3) | m3;
+  if (code > 0x7eu) code = 0x7eu;
+  return (u8)(sign | code);
+}
+
+FLIDE_DEV float e4m3fn_to_f32(u8 c) {
+  uint32_t s = (c & 0x80u) << 24;
+  uint32_t e = (c >> 3) & 0xfu;
+  uint32_t m = c & 7u;
+  if ((c & 0x7fu) == 0x7fu) return __uint_as_float(0x7fc00000u | s);
+  if (e == 0) return __uint_as_float(s) + (s ? -1.0f : 1.0f) * (float)m * 0.001953125f;
+  return __uint_as_float(s | ((e + 120u) << 23) | (m << 20));
+}
+
+// ---------------------------------------------------------------------------------------------------
+// wave64 reductions
+// ---------------------------------------------------------------------------------------------------
+FLIDE_DEV float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+FLIDE_DEV float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// (value, index) argmax over the wave: larger value wins, the lower index on equal values. Indices
+// of lanes with nothing left carry value -inf and index INT_MAX, so they never win over a real entry.
+FLIDE_DEV void wave_argmax(float& v, int& i) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    float ov = __shfl_xor(v, o, 64);
+    int oi = __shfl_xor(i, o, 64);
+    bool take = (ov > v) || (ov == v && oi < i);
+    v = take ? ov : v;
+    i = take ? oi : i;
+  }
+}
+
+FLIDE_DEV int lane_id() { return (int)__lane_id(); }
+
+// ---------------------------------------------------------------------------------------------------
+// MFMA fragments (gfx950)
+//
+// v_mfma_f32_16x16x32_{bf16,f16}: lane l holds 8 K-values of row (l % 16) of A and of column (l % 16)
+// of B, and 4 outputs D[(l / 16) * 4 + i][l % 16], i = 0..3. Which 8 K-values a lane holds only has
+// to agree between A and B. Every product here uses the same fixed assignment per 64-wide K chunk:
+// lane group g = l / 16 holds k = g*16 + s*8 + [0, 8) for the chunk's two MFMA steps s = 0, 1, and the
+// chunks run in ascending K. The sums therefore do not depend on the tile shape or on the number of
+// rows in a batch.
+//
+// v_mfma_f32_16x16x128_f8f6f4 (e4m3 x e4m3): lane l holds 32 bytes of row (l % 16) of A and of column
+// (l % 16) of B; lane group g holds k = g*32 + [0, 32) of each 128-wide K chunk.
+// ---------------------------------------------------------------------------------------------------
+template <typename T> struct Mfma16;
+
+template <> struct Mfma16<__bf16> {
+  static FLIDE_DEV f32x4_t mma(const u32x4_t& a, const u32x4_t& b, const f32x4_t& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+  }
+  static FLIDE_DEV float to_f32(u16 v) { return bf16_to_f32(v); }
+  static FLIDE_DEV u16 from_f32(float f) { return f32_to_bf16(f); }
+};
+
+template <> struct Mfma16<_Float16> {
+  static FLIDE_DEV f32x4_t mma(const u32x4_t& a, const u32x4_t& b, const f32x4_t& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+  }
+  static FLIDE_DEV float to_f32(u16 v) { return f16_to_f32(v); }
+  static FLIDE_DEV u16 from_f32(float f) { return f32_to_f16(f); }
+};
+
+FLIDE_DEV f32x4_t mfma_fp8(const i32x8_t& a, const i32x8_t& b, const f32x4_t& c) {
+  // format 0 = e4m3 for both operands; zero scale operands select the unscaled instruction
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+
+// ---------------------------------------------------------------------------------------------------
+// activations between the two grouped products (flide/kernels/pointwise.py:52-59,248-257)
+// ---------------------------------------------------------------------------------------------------
+// GELU-tanh(a) * b as 0.5 a (2 - 2 / (1 + e^{2z})), z = sqrt(2/pi) (a + 0.044715 a^3)
+FLIDE_DEV float geglu_f32(float a, float b) {
+  float z = 0.7978845608028654f * (a + 0.044715f * a * a * a);
+  float g = 0.5f * a * (2.0f - 2.0f / (1.0f + __expf(2.0f * z)));
+  return g * b;
+}
+
+FLIDE_DEV float swiglu_f32(float a, float b) { return a / (1.0f + __expf(-a)) * b; }
+
+enum { ACT_NONE = 0, ACT_GEGLU = 1, ACT_SWIGLU = 2 };
+
+template <int ACT> FLIDE_DEV float act_f32(float g, float u) {
+  if constexpr (ACT == ACT_GEGLU) return geglu_f32(g, u);
+  else return swiglu_f32(g, u);
+}
+
+// status helpers for the C ABI
+#define FLIDE_CHECK_LAUNCH()                                         \
+  do {                                                               \
+    hipError_t _e = hipGetLastError();                               \
+    if (_e != hipSuccess) return FLIDE_MOE_ERR_HIP_BASE + (int)_e;   \
+  } while (0)

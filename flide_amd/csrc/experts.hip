@@ -1,0 +1,103 @@
+// moe.experts in one C call (flide/kernels/moe.py:336-353): align, gate/up product with the fused
+// activation, down product times the routing weight; plus the float8 variant with its two
+// per-row quantizations (flide/kernels/moe.py:345-349, fp8.py:29-53). All scratch lives in the
+// caller's workspace, carved in the fixed order below, so the call allocates nothing and can be
+// captured into a HIP graph.
+#include "common.hpp"
+
+namespace {
+
+size_t align_up(size_t v) { return (v + 255) & ~(size_t)255; }
+
+struct ExpertsLayout {
+  size_t hist, rows, blocks, used, act, qx, sx, qa, sa, total;
+};
+
+ExpertsLayout layout(int T, int k, int E, int H, int I, int bm, int fp8) {
+  ExpertsLayout L{};
+  const long long n = (long long)T * k;
+  const long long total = (n + (long long)E * (bm - 1) + bm - 1) / bm * bm;
+  size_t off = 0;
+  L.hist = off;   off = align_up(off + flide_moe_align_workspace((int)n, E));
+  L.rows = off;   off = align_up(off + (size_t)total * 4);
+  L.blocks = off; off = align_up(off + (size_t)(total / bm) * 4);
+  L.used = off;   off = align_up(off + 4);
+  L.act = off;    off = align_up(off + (size_t)n * I * 2);
+  if (fp8) {
+    L.qx = off; off = align_up(off + (size_t)T * H);
+    L.sx = off; off = align_up(off + (size_t)T * 4);
+    L.qa = off; off = align_up(off + (size_t)n * I);
+    L.sa = off; off = align_up(off + (size_t)n * 4);
+  }
+  L.total = off;
+  return L;
+}
+
+}  // namespace
+
+extern "C" const char* flide_moe_strerror(int rc) {
+  switch (rc) {
+    case FLIDE_MOE_OK: return "ok";
+    case FLIDE_MOE_ERR_ARG: return "invalid argument (size, stride, alignment or dtype)";
+    case FLIDE_MOE_ERR_WORKSPACE: return "workspace too small";
+    case FLIDE_MOE_ERR_TILE: return "no kernel compiled for this tile shape";
+    default:
+      if (rc >= FLIDE_MOE_ERR_HIP_BASE) return hipGetErrorString((hipError_t)(rc - FLIDE_MOE_ERR_HIP_BASE));
+      return "unknown error";
+  }
+}
+
+extern "C" const char* flide_moe_version(void) { return "flide_moe 0.1 gfx950"; }
+
+extern "C" size_t flide_moe_experts_workspace(int T, int k, int E, int H, int I, int bm, int fp8) {
+  if (T < 0 || k <= 0 || E <= 0 || H <= 0 || I <= 0 || bm <= 0) return 0;
+  return layout(T, k, E, H, I, bm, fp8).total;
+}
+
+extern "C" int flide_moe_experts(const void* x, long long sx, int x_dtype, int T, int H,
+                                 const float* top, const int* ids, int k, const void* w_gu,
+                                 const void* w_d, const float* w_scale_gu, const float* w_scale_d,
+                                 int E, int I, void* y, int act, int bm, int bn, void* workspace,
+                                 size_t workspace_bytes, flide_stream_t stream) {
+  if (T < 0 || H <= 0 || k <= 0 || E <= 0 || I <= 0) return FLIDE_MOE_ERR_ARG;
+  if (x_dtype != FLIDE_BF16 && x_dtype != FLIDE_F16) return FLIDE_MOE_ERR_ARG;
+  if (act != ACT_GEGLU && act != ACT_SWIGLU) return FLIDE_MOE_ERR_ARG;
+  const int fp8 = w_scale_gu != nullptr;
+  if (fp8 != (w_scale_d != nullptr)) return FLIDE_MOE_ERR_ARG;
+  if (T == 0) return FLIDE_MOE_OK;
+  const ExpertsLayout L = layout(T, k, E, H, I, bm, fp8);
+  if (workspace_bytes < L.total) return FLIDE_MOE_ERR_WORKSPACE;
+  char* ws = (char*)workspace;
+  int* rows = (int*)(ws + L.rows);
+  int* blocks = (int*)(ws + L.blocks);
+  int* used = (int*)(ws + L.used);
+  void* actbuf = ws + L.act;
+  const int n = T * k;
+  const long long total = ((long long)n + (long long)E * (bm - 1) + bm - 1) / bm * bm;
+  const int nbm = (int)(total / bm);
+  int rc = flide_moe_align(ids, n, E, bm, rows, blocks, used, nullptr, ws + L.hist,
+                           L.rows - L.hist, stream);
+  if (rc) return rc;
+  if (!fp8) {
+    rc = flide_moe_grouped(x, sx, x_dtype, w_gu, (long long)2 * I * H, H, 2 * I, H, actbuf, I,
+                           x_dtype, nullptr, rows, blocks, used, n, nbm, k, 1, act, bm, bn, stream);
+    if (rc) return rc;
+    return flide_moe_grouped(actbuf, I, x_dtype, w_d, (long long)H * I, I, H, I, y, H, FLIDE_F32,
+                             top, rows, blocks, used, n, nbm, k, 0, ACT_NONE, bm, bn, stream);
+  }
+  u8* qx = (u8*)(ws + L.qx);
+  float* sxs = (float*)(ws + L.sx);
+  u8* qa = (u8*)(ws + L.qa);
+  float* sas = (float*)(ws + L.sa);
+  rc = flide_moe_quantize_rows(x, sx, T, H, x_dtype, qx, H, sxs, stream);
+  if (rc) return rc;
+  rc = flide_moe_grouped_fp8(qx, H, sxs, w_gu, (long long)2 * I * H, H, w_scale_gu, 2 * I, 2 * I, H,
+                             actbuf, I, x_dtype, nullptr, rows, blocks, used, n, nbm, k, 1, act, bm,
+                             bn, stream);
+  if (rc) return rc;
+  rc = flide_moe_quantize_rows(actbuf, I, n, I, x_dtype, qa, I, sas, stream);
+  if (rc) return rc;
+  return flide_moe_grouped_fp8(qa, I, sas, w_d, (long long)H * I, I, w_scale_d, H, H, I, y, H,
+                               x_dtype, top, rows, blocks, used, n, nbm, k, 0, ACT_NONE, bm, bn,
+                               stream);
+}

@@ -1,0 +1,275 @@
+// Row-wise kernels on the MoE path: combine_norm / combine (flide/kernels/moe.py:256-277,372-395),
+// per-row float8 quantization (flide/kernels/fp8.py:22-53), RMSNorm (flide/kernels/pointwise.py:21-49)
+// and the unfused gated activations (pointwise.py:52-69,248-268).
+//
+// One workgroup of 256 threads per row for the reductions. Rows are read with 16-byte vector loads
+// when the row length and stride allow it (every Gemma/Qwen shape does), else element by element.
+// All arithmetic is float32, rounded once at the store.
+#include "common.hpp"
+
+namespace {
+
+constexpr int RW_THREADS = 256;
+
+FLIDE_DEV float load_any(const void* p, int dtype, long long i) {
+  if (dtype == FLIDE_F32) return ((const float*)p)[i];
+  if (dtype == FLIDE_BF16) return bf16_to_f32(((const u16*)p)[i]);
+  return f16_to_f32(((const u16*)p)[i]);
+}
+
+FLIDE_DEV void store_any(void* p, int dtype, long long i, float v) {
+  if (dtype == FLIDE_F32) ((float*)p)[i] = v;
+  else if (dtype == FLIDE_BF16) ((u16*)p)[i] = f32_to_bf16(v);
+  else ((u16*)p)[i] = f32_to_f16(v);
+}
+
+// block-wide float sum (256 threads = 4 waves); every thread gets the total
+FLIDE_DEV float block_sum(float v, float* red) {
+  v = wave_sum(v);
+  const int wave = threadIdx.x >> 6, l = threadIdx.x & 63;
+  __syncthreads();
+  if (l == 0) red[wave] = v;
+  __syncthreads();
+  return red[0] + red[1] + red[2] + red[3];
+}
+
+FLIDE_DEV float block_max(float v, float* red) {
+  v = wave_max(v);
+  const int wave = threadIdx.x >> 6, l = threadIdx.x & 63;
+  __syncthreads();
+  if (l == 0) red[wave] = v;
+  __syncthreads();
+  return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+// ---------------------------------------------------------------------------------------------------
+// combine_norm: one workgroup per token; the token's k rows summed in slot order into registers
+// ---------------------------------------------------------------------------------------------------
+constexpr int CN_MAXV = 8;  // up to 256 * 8 * 4 = 8192 columns with float4 pieces
+
+template <int YDT>
+__global__ __launch_bounds__(RW_THREADS) void combine_norm_kernel(const void* __restrict__ y,
+                                                                  const void* __restrict__ dense,
+                                                                  long long sd, const void* w1,
+                                                                  const void* w2, int w_dtype,
+                                                                  void* __restrict__ out, long long so,
+                                                                  int out_dtype, int H, int k,
+                                                                  float eps) {
+  __shared__ float red[4];
+  const long long t = blockIdx.x;
+  const int nv = H / 4;  // float4 pieces (H % 4 == 0 checked on the host)
+  float4 acc[CN_MAXV];
+  float ss = 0.f;
+#pragma unroll
+  for (int v = 0; v < CN_MAXV; ++v) {
+    const int c4 = threadIdx.x + v * RW_THREADS;
+    float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (c4 < nv) {
+      for (int j = 0; j < k; ++j) {
+        const long long row = (t * k + j) * (long long)H;
+        float4 yv;
+        if constexpr (YDT == FLIDE_F32) {
+          yv = ((const float4*)((const float*)y + row))[c4];
+        } else {
+          uint2 raw = ((const uint2*)((const u16*)y + row))[c4];
+          if constexpr (YDT == FLIDE_BF16) {
+            yv = make_float4(bf16_to_f32(raw.x & 0xffff), bf16_to_f32(raw.x >> 16),
+                             bf16_to_f32(raw.y & 0xffff), bf16_to_f32(raw.y >> 16));
+          } else {
+            yv = make_float4(f16_to_f32(raw.x & 0xffff), f16_to_f32(raw.x >> 16),
+                             f16_to_f32(raw.y & 0xffff), f16_to_f32(raw.y >> 16));
+          }
+        }
+        s.x += yv.x; s.y += yv.y; s.z += yv.z; s.w += yv.w;
+      }
+      ss += s.x * s.x + s.y * s.y + s.z * s.z + s.w * s.w;
+    }
+    acc[v] = s;
+  }
+  float dd = 0.f;
+  for (int c = threadIdx.x; c < H; c += RW_THREADS) {
+    float d = load_any(dense, out_dtype, t * sd + c);
+    dd += d * d;
+  }
+  const float sum_ss = block_sum(ss, red);
+  const float sum_dd = block_sum(dd, red);
+  const float inv_b = rsqrtf(sum_ss / H + eps);
+  const float inv_a = rsqrtf(sum_dd / H + eps);
+#pragma unroll
+  for (int v = 0; v < CN_MAXV; ++v) {
+    const int c4 = threadIdx.x + v * RW_THREADS;
+    if (c4 >= nv) continue;
+    const float vals[4] = {acc[v].x, acc[v].y, acc[v].z, acc[v].w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int c = c4 * 4 + q;
+      const float d = load_any(dense, out_dtype, t * sd + c);
+      const float a = d * inv_a * load_any(w1, w_dtype, c);
+      const float b = vals[q] * inv_b * load_any(w2, w_dtype, c);
+      store_any(out, out_dtype, t * so + c, a + b);
+    }
+  }
+}
+
+// combine (Qwen): sum of the k rows + shared * sigmoid(gate); one workgroup per (token, 1024 columns)
+template <int YDT>
+__global__ __launch_bounds__(RW_THREADS) void combine_kernel(const void* __restrict__ y,
+                                                             const void* __restrict__ shared,
+                                                             const float* __restrict__ gate,
+                                                             void* __restrict__ out, int out_dtype,
+                                                             int H, int k) {
+  const long long t = blockIdx.x;
+  const float gt = gate[t];
+  const float sg = 1.0f / (1.0f + expf(-gt));
+  for (int c = blockIdx.y * 1024 + threadIdx.x; c < min(H, (int)(blockIdx.y + 1) * 1024);
+       c += RW_THREADS) {
+    float s = 0.f;
+    for (int j = 0; j < k; ++j) s += load_any(y, YDT, (t * k + j) * (long long)H + c);
+    const float sh = load_any(shared, out_dtype, t * H + c);
+    store_any(out, out_dtype, t * H + c, s + sh * sg);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------
+// per-row e4m3 quantization: s = max(amax, 1e-12) * (1/448); q = e4m3(clamp(x / s, +-448))
+// ---------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(RW_THREADS) void quantize_rows_kernel(const void* __restrict__ x,
+                                                                   long long sx, int K, int x_dtype,
+                                                                   u8* __restrict__ q, long long sq,
+                                                                   float* __restrict__ s) {
+  __shared__ float red[4];
+  const long long row = blockIdx.x;
+  float amax = 0.f;
+  for (int c = threadIdx.x; c < K; c += RW_THREADS)
+    amax = fmaxf(amax, fabsf(load_any(x, x_dtype, row * sx + c)));
+  amax = block_max(amax, red);
+  const float sc = fmaxf(amax, 1e-12f) * (1.0f / 448.0f);
+  if (threadIdx.x == 0) s[row] = sc;
+  for (int c = threadIdx.x; c < K; c += RW_THREADS) {
+    float v = load_any(x, x_dtype, row * sx + c) / sc;  // correctly rounded division
+    v = fminf(fmaxf(v, -448.0f), 448.0f);
+    q[row * sq + c] = f32_to_e4m3fn(v);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------
+// RMSNorm without residual
+// ---------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(RW_THREADS) void rms_norm_kernel(const void* __restrict__ x, long long sx,
+                                                              int x_dtype, const void* w, int w_dtype,
+                                                              void* __restrict__ yout, long long sy,
+                                                              int y_dtype, int N, float eps,
+                                                              int offset) {
+  __shared__ float red[4];
+  const long long row = blockIdx.x;
+  float ss = 0.f;
+  for (int c = threadIdx.x; c < N; c += RW_THREADS) {
+    float v = load_any(x, x_dtype, row * sx + c);
+    ss += v * v;
+  }
+  ss = block_sum(ss, red);
+  const float inv = rsqrtf(ss / N + eps);
+  for (int c = threadIdx.x; c < N; c += RW_THREADS) {
+    float v = load_any(x, x_dtype, row * sx + c);
+    float wv = load_any(w, w_dtype, c);
+    if (offset) wv = 1.0f + wv;
+    store_any(yout, y_dtype, row * sy + c, v * inv * wv);
+  }
+}
+
+template <int ACT>
+__global__ __launch_bounds__(RW_THREADS) void gated_act_kernel(const void* __restrict__ a,
+                                                               long long sa,
+                                                               const void* __restrict__ b,
+                                                               long long sb, void* __restrict__ out,
+                                                               long long so, int dtype, int n) {
+  const long long row = blockIdx.x;
+  for (int c = blockIdx.y * 1024 + threadIdx.x; c < min(n, (int)(blockIdx.y + 1) * 1024);
+       c += RW_THREADS) {
+    const float av = load_any(a, dtype, row * sa + c);
+    const float bv = load_any(b, dtype, row * sb + c);
+    store_any(out, dtype, row * so + c, act_f32<ACT>(av, bv));
+  }
+}
+
+bool dtype_ok(int d) { return d == FLIDE_F32 || d == FLIDE_BF16 || d == FLIDE_F16; }
+
+}  // namespace
+
+extern "C" int flide_moe_combine_norm(const void* y, int y_dtype, const void* dense, long long sd,
+                                      const void* w1, const void* w2, int w_dtype, void* out,
+                                      long long so, int out_dtype, int T, int H, int k, float eps,
+                                      flide_stream_t stream) {
+  if (T < 0 || H <= 0 || k <= 0 || H % 4 || H > 4 * RW_THREADS * CN_MAXV) return FLIDE_MOE_ERR_ARG;
+  if (!dtype_ok(y_dtype) || !dtype_ok(w_dtype) || !dtype_ok(out_dtype)) return FLIDE_MOE_ERR_ARG;
+  if ((uintptr_t)y & 15) return FLIDE_MOE_ERR_ARG;
+  if (T == 0) return FLIDE_MOE_OK;
+  hipStream_t st = (hipStream_t)stream;
+  if (y_dtype == FLIDE_F32)
+    combine_norm_kernel<FLIDE_F32><<<T, RW_THREADS, 0, st>>>(y, dense, sd, w1, w2, w_dtype, out, so,
+                                                              out_dtype, H, k, eps);
+  else if (y_dtype == FLIDE_BF16)
+    combine_norm_kernel<FLIDE_BF16><<<T, RW_THREADS, 0, st>>>(y, dense, sd, w1, w2, w_dtype, out, so,
+                                                               out_dtype, H, k, eps);
+  else
+    combine_norm_kernel<FLIDE_F16><<<T, RW_THREADS, 0, st>>>(y, dense, sd, w1, w2, w_dtype, out, so,
+                                                              out_dtype, H, k, eps);
+  FLIDE_CHECK_LAUNCH();
+  return FLIDE_MOE_OK;
+}
+
+extern "C" int flide_moe_combine(const void* y, int y_dtype, const void* shared, const float* gate,
+                                 void* out, int out_dtype, int T, int H, int k,
+                                 flide_stream_t stream) {
+  if (T < 0 || H <= 0 || k <= 0 || !dtype_ok(y_dtype) || !dtype_ok(out_dtype))
+    return FLIDE_MOE_ERR_ARG;
+  if (T == 0) return FLIDE_MOE_OK;
+  hipStream_t st = (hipStream_t)stream;
+  dim3 grid(T, (H + 1023) / 1024);
+  if (y_dtype == FLIDE_F32)
+    combine_kernel<FLIDE_F32><<<grid, RW_THREADS, 0, st>>>(y, shared, gate, out, out_dtype, H, k);
+  else if (y_dtype == FLIDE_BF16)
+    combine_kernel<FLIDE_BF16><<<grid, RW_THREADS, 0, st>>>(y, shared, gate, out, out_dtype, H, k);
+  else
+    combine_kernel<FLIDE_F16><<<grid, RW_THREADS, 0, st>>>(y, shared, gate, out, out_dtype, H, k);
+  FLIDE_CHECK_LAUNCH();
+  return FLIDE_MOE_OK;
+}
+
+extern "C" int flide_moe_quantize_rows(const void* x, long long sx, int M, int K, int x_dtype,
+                                       void* q, long long sq, float* s, flide_stream_t stream) {
+  if (M < 0 || K < 0 || !dtype_ok(x_dtype)) return FLIDE_MOE_ERR_ARG;
+  if (M == 0) return FLIDE_MOE_OK;
+  quantize_rows_kernel<<<M, RW_THREADS, 0, (hipStream_t)stream>>>(x, sx, K, x_dtype, (u8*)q, sq, s);
+  FLIDE_CHECK_LAUNCH();
+  return FLIDE_MOE_OK;
+}
+
+extern "C" int flide_moe_rms_norm(const void* x, long long sx, int x_dtype, const void* w,
+                                  int w_dtype, void* y, long long sy, int y_dtype, int T, int N,
+                                  float eps, int offset, flide_stream_t stream) {
+  if (T < 0 || N <= 0 || !dtype_ok(x_dtype) || !dtype_ok(w_dtype) || !dtype_ok(y_dtype))
+    return FLIDE_MOE_ERR_ARG;
+  if (T == 0) return FLIDE_MOE_OK;
+  rms_norm_kernel<<<T, RW_THREADS, 0, (hipStream_t)stream>>>(x, sx, x_dtype, w, w_dtype, y, sy,
+                                                             y_dtype, N, eps, offset);
+  FLIDE_CHECK_LAUNCH();
+  return FLIDE_MOE_OK;
+}
+
+extern "C" int flide_moe_gated_act(const void* a, long long sa, const void* b, long long sb,
+                                   void* out, long long so, int dtype, int T, int n, int act,
+                                   flide_stream_t stream) {
+  if (T < 0 || n < 0 || !dtype_ok(dtype)) return FLIDE_MOE_ERR_ARG;
+  if (T == 0 || n == 0) return FLIDE_MOE_OK;
+  dim3 grid(T, (n + 1023) / 1024);
+  hipStream_t st = (hipStream_t)stream;
+  if (act == ACT_GEGLU)
+    gated_act_kernel<ACT_GEGLU><<<grid, RW_THREADS, 0, st>>>(a, sa, b, sb, out, so, dtype, n);
+  else if (act == ACT_SWIGLU)
+    gated_act_kernel<ACT_SWIGLU><<<grid, RW_THREADS, 0, st>>>(a, sa, b, sb, out, so, dtype, n);
+  else
+    return FLIDE_MOE_ERR_ARG;
+  FLIDE_CHECK_LAUNCH();
+  return FLIDE_MOE_OK;
+}

@@ -1,0 +1,301 @@
+"""GPU parity: the HIP path (through the C ABI, via flide_amd.kernels) against the CPU oracle on the same
+seeded inputs. Routing ids, counts and the permutation are compared bit-exactly; outputs within 1e-2
+relative for 16-bit experts and 3e-2 for FP8 experts."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import moe_oracle as orc
+from tests.helpers import assert_close, inputs, logits_only, np32
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+REL_BF16 = 1e-2
+REL_FP8 = 3e-2
+
+
+def _moe():
+    from flide_amd.kernels import moe
+
+    return moe
+
+
+def _gelu_act(gu, n):
+    from flide_amd.kernels import pointwise as pw
+
+    return pw.geglu(gu[:, :n], gu[:, n:])
+
+
+# --------------------------------------------------------------------------------------------------
+# routing
+# --------------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("T,E,k", [(1, 16, 2), (64, 128, 8), (300, 96, 6), (257, 1000, 4), (8, 8, 8), (33, 5, 1)])
+def test_route_matches_oracle(T, E, k):
+    print(f"route T={T} E={E} k={k}", flush=True)
+    g = torch.Generator().manual_seed(T * 7 + E)
+    logits = torch.randn(T, E, generator=g)
+    scale = torch.rand(E, generator=g) + 0.5
+    w, ids = _moe().route(logits.to(DEV), k, scale.to(DEV))
+    rw, rids = orc.route(logits.numpy(), k, scale.numpy())
+    np.testing.assert_array_equal(ids.cpu().numpy(), rids)
+    np.testing.assert_allclose(w.cpu().numpy(), rw, rtol=1e-5, atol=1e-7)
+
+
+def test_route_ties_go_to_lower_id():
+    print("route ties", flush=True)
+    g = torch.Generator().manual_seed(5)
+    logits = torch.randint(-3, 3, (512, 128), generator=g).float()   # heavy exact ties
+    logits[0] = 0.0                                                   # all equal: ids 0..k-1, weights 1/k
+    w, ids = _moe().route(logits.to(DEV), 8)
+    rw, rids = orc.route(logits.numpy(), 8)
+    np.testing.assert_array_equal(ids.cpu().numpy(), rids)
+    np.testing.assert_array_equal(ids.cpu().numpy()[0], np.arange(8))
+    np.testing.assert_allclose(w.cpu().numpy(), rw, rtol=1e-5, atol=1e-7)
+    np.testing.assert_allclose(w.cpu().numpy()[0], np.full(8, 1 / 8), rtol=1e-6)
+
+
+@pytest.mark.parametrize("cfg", [1, 2, 3, 4])
+def test_route_configs_exact(cfg):
+    print(f"route cfg{cfg}", flush=True)
+    d = logits_only(cfg)
+    c = d["cfg"]
+    w, ids = _moe().route(d["logits"].to(DEV), c.k)
+    rw, rids = orc.route(d["logits"].numpy(), c.k)
+    np.testing.assert_array_equal(ids.cpu().numpy(), rids)
+    np.testing.assert_allclose(w.cpu().numpy(), rw, rtol=1e-5, atol=1e-7)
+
+
+# --------------------------------------------------------------------------------------------------
+# align
+# --------------------------------------------------------------------------------------------------
+def _check_align(ids_np, E, bm):
+    moe = _moe()
+    ids = torch.from_numpy(ids_np.astype(np.int32)).to(DEV)
+    counts = torch.full((E,), -7, dtype=torch.int32, device=DEV)
+    rows, blocks, used = moe.align(ids, E, bm, counts=counts)
+    ref = orc.align(ids_np, E, bm)
+    u = int(used.item())
+    assert u == int(ref["used"][0])
+    assert rows.shape[0] == ref["total"] and blocks.shape[0] == ref["total"] // bm
+    np.testing.assert_array_equal(rows.cpu().numpy()[:u], ref["rows"][:u])
+    np.testing.assert_array_equal(blocks.cpu().numpy()[:u // bm], ref["blocks"][:u // bm])
+    np.testing.assert_array_equal(counts.cpu().numpy(), ref["counts"])
+
+
+@pytest.mark.parametrize("T,E,k,bm", [(64, 128, 8, 16), (256, 16, 2, 64), (5000, 128, 8, 128), (3, 7, 2, 1),
+                                      (1000, 1000, 4, 32), (2048, 128, 8, 128)])
+def test_align_random(T, E, k, bm):
+    print(f"align T={T} E={E} k={k} bm={bm}", flush=True)
+    rng = np.random.default_rng(T + E)
+    ids = np.stack([rng.permutation(E)[:k] for _ in range(T)])
+    _check_align(ids, E, bm)
+
+
+def test_align_skewed_and_empty():
+    print("align skew", flush=True)
+    rng = np.random.default_rng(3)
+    ids = np.zeros((4099, 4), np.int64)
+    ids[:, 0] = 5                                    # one expert takes every token
+    ids[:, 1:] = rng.integers(6, 9, (4099, 3))       # experts 0..4 and 9.. stay empty
+    _check_align(ids, 16, 64)
+
+
+@pytest.mark.parametrize("cfg", [1, 2, 4])
+def test_align_configs_exact(cfg):
+    print(f"align cfg{cfg}", flush=True)
+    d = logits_only(cfg)
+    c = d["cfg"]
+    _, rids = orc.route(d["logits"].numpy(), c.k)
+    bm = _moe().tile(c.pairs, False)[0]
+    _check_align(rids, c.E, bm)
+
+
+# --------------------------------------------------------------------------------------------------
+# grouped products and the experts
+# --------------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("bm", [16, 32, 64, 128])
+@pytest.mark.parametrize("by_token,mul_w,out32", [(True, False, False), (False, True, True)])
+def test_grouped_bf16(bm, by_token, mul_w, out32):
+    print(f"grouped bm={bm} by_token={by_token}", flush=True)
+    moe = _moe()
+    g = torch.Generator().manual_seed(bm)
+    T, E, k, N, K = 96, 12, 3, 200, 136
+    logits = torch.randn(T, E, generator=g)
+    _, ids = orc.route(logits.numpy(), k)
+    rows_in = T if by_token else T * k
+    a = torch.randn(rows_in, K, generator=g).to(torch.bfloat16)
+    w = (torch.randn(E, N, K, generator=g) * 0.05).to(torch.bfloat16)
+    wts = torch.rand(T * k, generator=g)
+    rows, blocks, used = moe.align(torch.from_numpy(ids).to(DEV), E, bm)
+    out = torch.full((T * k, N), float("nan"), device=DEV, dtype=torch.float32 if out32 else torch.bfloat16)
+    moe.grouped(a.to(DEV), w.to(DEV), out, rows, blocks, used, k, by_token, wts.to(DEV) if mul_w else None,
+                tile=(bm, 128, 4, 2))
+    al = orc.align(ids, E, bm)
+    ref = orc.grouped(np32(a), np32(w), al["rows"], al["blocks"], al["used"], T * k, k, by_token,
+                      wts.numpy() if mul_w else None, bm=bm, out_dtype="fp32" if out32 else "bf16")
+    assert_close(np32(out), ref, REL_BF16 if not out32 else 1e-5, "grouped")
+
+
+def _experts_case(cfg, T=None, pairs_subset=None, fp8=False):
+    moe = _moe()
+    d = inputs(cfg, 0, T)
+    c = d["cfg"]
+    T = d["T"]
+    top, ids = moe.route(d["logits"].to(DEV), c.k)
+    w = {"experts": d["w_gu"].to(DEV), "experts_down": d["w_d"].to(DEV), "inter": c.I}
+    if fp8:
+        w["experts_scale"] = d["w_gu_scale"].to(DEV)
+        w["experts_down_scale"] = d["w_d_scale"].to(DEV)
+    y = moe.experts(d["x"].to(DEV), w, top, ids, _gelu_act)
+    torch.cuda.synchronize()
+    rtop, rids = orc.route(d["logits"].numpy(), c.k)
+    np.testing.assert_array_equal(ids.cpu().numpy(), rids)
+    if fp8:
+        ref = orc.experts_fp8(np32(d["x"]), np32(d["w_gu"]), d["w_gu_scale"].numpy(), np32(d["w_d"]),
+                              d["w_d_scale"].numpy(), rtop, rids, c.I, "geglu", pairs=pairs_subset)
+    else:
+        ref = orc.experts(np32(d["x"]), np32(d["w_gu"]), np32(d["w_d"]), rtop, rids, c.I, "geglu", "bf16",
+                          pairs=pairs_subset)
+    sel = slice(None) if pairs_subset is None else pairs_subset
+    return np32(y)[sel], ref[sel], y
+
+
+def test_experts_cfg1_decode():
+    print("experts cfg1", flush=True)
+    got, ref, _ = _experts_case(1)
+    assert_close(got, ref, REL_BF16, "experts cfg1")
+
+
+def test_experts_cfg1_shape_other_tiles():
+    """T = 512 and 2048 at the Gemma shape run the bm 32 / 64 / 128 kernels."""
+    for T in (512, 2048, 4096):
+        print(f"experts cfg1 T={T}", flush=True)
+        sub = np.random.default_rng(T).choice(T * 8, 256, replace=False)
+        got, ref, _ = _experts_case(1, T=T, pairs_subset=np.sort(sub))
+        assert_close(got, ref, REL_BF16, f"experts T={T}")
+
+
+def test_experts_cfg3_fp8_subset():
+    print("experts cfg3 fp8 T=512", flush=True)
+    sub = np.sort(np.random.default_rng(0).choice(512 * 8, 512, replace=False))
+    got, ref, _ = _experts_case(3, T=512, pairs_subset=sub, fp8=True)
+    assert_close(got, ref, REL_FP8, "experts fp8")
+
+
+def test_experts_cfg3_fp8_decode_tile():
+    print("experts cfg3 fp8 T=64", flush=True)
+    got, ref, _ = _experts_case(3, T=64, fp8=True)
+    assert_close(got, ref, REL_FP8, "experts fp8 T=64")
+
+
+# --------------------------------------------------------------------------------------------------
+# combine, quantize, router, norms
+# --------------------------------------------------------------------------------------------------
+def test_combine_norm():
+    print("combine_norm", flush=True)
+    moe = _moe()
+    g = torch.Generator().manual_seed(11)
+    T, H, k = 37, 2816, 8
+    y = torch.randn(T * k, H, generator=g)
+    dense = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    w1 = (torch.rand(H, generator=g) + 0.5).to(torch.bfloat16)
+    w2 = (torch.rand(H, generator=g) + 0.5).to(torch.bfloat16)
+    out = moe.combine_norm(y.to(DEV), dense.to(DEV), w1.to(DEV), w2.to(DEV), k, 1e-6)
+    ref = orc.combine_norm(y.numpy(), np32(dense), np32(w1), np32(w2), k, 1e-6)
+    assert_close(np32(out), ref, 1e-2, "combine_norm")
+    # one bf16 rounding: at most 1 ulp from the float64 reference
+    np.testing.assert_allclose(np32(out), ref, rtol=2 ** -7, atol=1e-6)
+
+
+def test_combine_qwen():
+    print("combine", flush=True)
+    moe = _moe()
+    g = torch.Generator().manual_seed(12)
+    T, H, k = 19, 2048 + 64, 4
+    y = torch.randn(T * k, H, generator=g)
+    shared = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    gate = torch.randn(T, 1, generator=g)
+    out = moe.combine(y.to(DEV), shared.to(DEV), gate.to(DEV), k)
+    ref = orc.combine(y.numpy(), np32(shared), gate.numpy(), k)
+    np.testing.assert_allclose(np32(out), ref, rtol=2 ** -7, atol=1e-6)
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
+def test_quantize_rows_bit_exact(dt):
+    print(f"quantize {dt}", flush=True)
+    from flide_amd.kernels import fp8
+
+    g = torch.Generator().manual_seed(13)
+    x = torch.randn(97, 704, generator=g) * torch.logspace(-6, 3, 97).unsqueeze(1)
+    x[3] = 0.0
+    x[5, :10] = torch.tensor([448.0, -448.0, 1e-30, -1e-30, 0.0, -0.0, 3.0, 5e-3, 1e-8, 2.0])
+    x = x.to(dt)
+    q, s = fp8.quantize_tokens(x.to(DEV))
+    rq, rs = orc.quantize_rows(np32(x))
+    np.testing.assert_array_equal(s.cpu().numpy(), rs)
+    np.testing.assert_array_equal(q.cpu().view(torch.uint8).numpy(), orc.e4m3fn_encode(rq))
+
+
+def test_quantize_experts_matches_rows():
+    print("quantize_experts", flush=True)
+    moe = _moe()
+    g = torch.Generator().manual_seed(14)
+    w = (torch.randn(4, 64, 256, generator=g) * 0.02).to(torch.bfloat16)
+    q, s = moe.quantize_experts(w.to(DEV))
+    rq, rs = orc.quantize_experts(np32(w))
+    np.testing.assert_array_equal(s.cpu().numpy(), rs)
+    np.testing.assert_array_equal(q.cpu().view(torch.uint8).numpy(), orc.e4m3fn_encode(rq))
+
+
+def test_router_logits():
+    print("router", flush=True)
+    moe = _moe()
+    g = torch.Generator().manual_seed(15)
+    T, H, E = 77, 2816, 128
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    wr = (torch.randn(E, H, generator=g) * 0.02).to(torch.bfloat16)
+    wg = (torch.randn(H, generator=g) * 0.02).to(torch.bfloat16)
+    logits, gate = moe.router(x.to(DEV), wr.to(DEV), wg.to(DEV))
+    rl, rg = orc.router(np32(x), np32(wr), np32(wg))
+    np.testing.assert_allclose(logits.cpu().numpy(), rl, rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(gate.cpu().numpy(), rg, rtol=1e-5, atol=1e-5)
+
+
+def test_rms_norm_and_geglu():
+    print("rms_norm/geglu", flush=True)
+    from flide_amd.kernels import pointwise as pw
+
+    g = torch.Generator().manual_seed(16)
+    h = torch.randn(33, 2816, generator=g).to(torch.bfloat16)
+    wn = torch.rand(2816, generator=g) * 0.05
+    y = pw.rms_norm(h.to(DEV), wn.to(DEV), 1e-6, offset=False)
+    ref = orc.rms_norm(np32(h), wn.numpy(), 1e-6, offset=False)
+    np.testing.assert_allclose(np32(y), ref, rtol=2 ** -7, atol=1e-7)
+    gu = (torch.randn(50, 2 * 704, generator=g) * 2).to(torch.bfloat16)
+    a = pw.geglu(gu[:, :704].to(DEV), gu[:, 704:].to(DEV))
+    ra = orc.geglu(np32(gu[:, :704]), np32(gu[:, 704:]))
+    # GELU-tanh as 2 - 2/(1 + e^{2z}) cancels for large negative gates: absolute floor 1e-5
+    np.testing.assert_allclose(np32(a), ra, rtol=2 ** -7, atol=1e-5)
+
+
+# --------------------------------------------------------------------------------------------------
+# whole layer
+# --------------------------------------------------------------------------------------------------
+def test_layer_cfg1_route_experts_combine():
+    print("layer cfg1", flush=True)
+    moe = _moe()
+    d = inputs(1)
+    c = d["cfg"]
+    top, ids = moe.route(d["logits"].to(DEV), c.k)
+    w = {"experts": d["w_gu"].to(DEV), "experts_down": d["w_d"].to(DEV), "inter": c.I}
+    y = moe.experts(d["x"].to(DEV), w, top, ids, _gelu_act)
+    dense = d["x"].to(DEV)
+    ones = torch.ones(c.H, dtype=torch.bfloat16, device=DEV)
+    out = moe.combine_norm(y, dense, ones, ones, c.k, 1e-6)
+    rtop, rids = orc.route(d["logits"].numpy(), c.k)
+    ry = orc.experts(np32(d["x"]), np32(d["w_gu"]), np32(d["w_d"]), rtop, rids, c.I, "geglu", "bf16")
+    ref = orc.combine_norm(ry, np32(d["x"]), np.ones(c.H), np.ones(c.H), c.k, 1e-6)
+    assert_close(np32(out), ref, REL_BF16, "layer cfg1")
