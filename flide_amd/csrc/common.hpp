@@ -106,13 +106,13 @@ FLIDE_DEV int lane_id() { return (int)__lane_id(); }
 //
 // v_mfma_f32_16x16x32_{bf16,f16}: lane l holds 8 K-values of row (l % 16) of A and of column (l % 16)
 // of B, and 4 outputs D[(l / 16) * 4 + i][l % 16], i = 0..3. Which 8 K-values a lane holds only has
-// to agree between A and B. Every product here uses the same fixed assignment per 64-wide K chunk:
-// lane group g = l / 16 holds k = g*16 + s*8 + [0, 8) for the chunk's two MFMA steps s = 0, 1, and the
-// chunks run in ascending K. The sums therefore do not depend on the tile shape or on the number of
-// rows in a batch.
+// to agree between A and B. Every 16-bit product here uses the same fixed assignment: for each 32-wide
+// K step c (in ascending order, one MFMA each), lane group g = l / 16 holds k = c*32 + g*8 + [0, 8).
+// The sums therefore do not depend on the kernel, the tile shape or the number of rows in a batch.
 //
 // v_mfma_f32_16x16x128_f8f6f4 (e4m3 x e4m3): lane l holds 32 bytes of row (l % 16) of A and of column
-// (l % 16) of B; lane group g holds k = g*32 + [0, 32) of each 128-wide K chunk.
+// (l % 16) of B; here lane group g holds k = g*16 + [0, 16) and 64 + g*16 + [0, 16) of each 128-wide
+// K chunk (two 16-byte pieces whose LDS reads are bank-conflict-free), chunks in ascending K.
 // ---------------------------------------------------------------------------------------------------
 template <typename T> struct Mfma16;
 

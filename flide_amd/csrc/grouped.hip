@@ -19,86 +19,12 @@
 // rows of the same output columns (rows c and c + N/2), each wave holds matching gate and up
 // fragments, and the epilogue rounds both to the 16-bit type (as the reference stores gu) before
 // act(gate, up) is applied and rounded once. gu is never written to memory.
-#include "common.hpp"
+#include <stdlib.h>
+
+#include "grouped_common.hpp"
 
 namespace {
-
-constexpr int LDK = 64 + 8;      // LDS row pitch (u16) for the 16-bit kernels: 144 bytes
-constexpr int LDK8 = 128 + 16;   // LDS row pitch (bytes) for the float8 kernels
-
-template <typename OutT> FLIDE_DEV OutT cvt_out(float v);
-template <> FLIDE_DEV float cvt_out<float>(float v) { return v; }
-
-struct Bf16Out { u16 v; };
-struct F16Out { u16 v; };
-
-template <typename OutT> struct OutTraits;
-template <> struct OutTraits<float> {
-  typedef float storage;
-  static FLIDE_DEV float conv(float v) { return v; }
-  static FLIDE_DEV float round16(float v) { return v; }
-};
-template <> struct OutTraits<Bf16Out> {
-  typedef u16 storage;
-  static FLIDE_DEV u16 conv(float v) { return f32_to_bf16(v); }
-};
-template <> struct OutTraits<F16Out> {
-  typedef u16 storage;
-  static FLIDE_DEV u16 conv(float v) { return f32_to_f16(v); }
-};
-
-// rounding of gu to the activation dtype before the fused activation
-template <typename T> FLIDE_DEV float round_in(float v);
-template <> FLIDE_DEV float round_in<__bf16>(float v) { return bf16_to_f32(f32_to_bf16(v)); }
-template <> FLIDE_DEV float round_in<_Float16>(float v) { return f16_to_f32(f32_to_f16(v)); }
-
-struct GroupArgs {
-  const void* a;       // activations [*, K]
-  long long sa;
-  const void* w;       // weights [E, N, K]
-  long long sbe, sbn;
-  const float* a_scale;  // fp8: per-row scales of a
-  const float* w_scale;  // fp8: [E, N]
-  long long sse;
-  int N, K;
-  void* out;
-  long long sc;
-  const float* weights;
-  const int* rows;
-  const int* blocks;
-  const int* used;
-  int n_pairs, nbm, topk, by_token;
-  int ntn;             // column tiles
-};
-
-// ---------------------------------------------------------------------------------------------------
-// shared epilogue: one 16x16 fragment pair (or single fragment) of a block
-// ---------------------------------------------------------------------------------------------------
-// Row of the tile that output register i of lane l holds: (l / 16) * 4 + i; column: l % 16.
-template <typename OutT, int ACT, typename T>
-FLIDE_DEV void store_frag(const GroupArgs& p, const int* s_pairs, int row0, int col, const f32x4_t& g,
-                          const f32x4_t& u, float colscale_g, float colscale_u, const float* rowscale,
-                          bool col_ok) {
-  typedef typename OutTraits<OutT>::storage S;
-  const int l = lane_id();
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int tr = row0 + (l >> 4) * 4 + i;
-    const int pair = s_pairs[tr];
-    if (pair >= p.n_pairs || !col_ok) continue;
-    float v;
-    if constexpr (ACT == ACT_NONE) {
-      v = g[i] * rowscale[i] * colscale_g;
-      if (p.weights) v *= p.weights[pair];
-    } else {
-      float gg = round_in<T>(g[i] * rowscale[i] * colscale_g);
-      float uu = round_in<T>(u[i] * rowscale[i] * colscale_u);
-      v = act_f32<ACT>(gg, uu);
-      if (p.weights) v *= p.weights[pair];
-    }
-    ((S*)p.out)[(long long)pair * p.sc + col] = OutTraits<OutT>::conv(v);
-  }
-}
+using namespace grouped_detail;
 
 // ---------------------------------------------------------------------------------------------------
 // LDS-tiled 16-bit kernel (prefill)
@@ -217,10 +143,10 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void grouped_lds16(GroupArgs
       u32x4_t af[FM], bfr[FN];
 #pragma unroll
       for (int fm = 0; fm < FM; ++fm)
-        af[fm] = *(const u32x4_t*)(&As[buf][(wm * WM + fm * 16 + r) * LDK + g * 16 + s * 8]);
+        af[fm] = *(const u32x4_t*)(&As[buf][(wm * WM + fm * 16 + r) * LDK + s * 32 + g * 8]);
 #pragma unroll
       for (int fn = 0; fn < FN; ++fn)
-        bfr[fn] = *(const u32x4_t*)(&Bs[buf][(brow[fn] + r) * LDK + g * 16 + s * 8]);
+        bfr[fn] = *(const u32x4_t*)(&Bs[buf][(brow[fn] + r) * LDK + s * 32 + g * 8]);
 #pragma unroll
       for (int fm = 0; fm < FM; ++fm)
 #pragma unroll
@@ -281,7 +207,7 @@ __global__ __launch_bounds__(256) void grouped_stream16(GroupArgs p) {
     int pair = s_pairs[fm * 16 + r];
     a_ok[fm] = pair < p.n_pairs;
     long long src = p.by_token ? pair / p.topk : pair;
-    a_src[fm] = A + (a_ok[fm] ? src * p.sa : 0) + g * 16;
+    a_src[fm] = A + (a_ok[fm] ? src * p.sa : 0) + g * 8;
   }
   const u16* b_src[NF];
   bool b_ok[NF];
@@ -301,7 +227,7 @@ __global__ __launch_bounds__(256) void grouped_stream16(GroupArgs p) {
       n = f < H2 ? c : c + half;
       colv[f] = c;
     }
-    b_src[f] = B + (b_ok[f] ? n * p.sbn : 0) + g * 16;
+    b_src[f] = B + (b_ok[f] ? n * p.sbn : 0) + g * 8;
   }
 
   f32x4_t acc[FM][NF];
@@ -315,19 +241,19 @@ __global__ __launch_bounds__(256) void grouped_stream16(GroupArgs p) {
     u32x4_t bb[U][NF][2], aa[U][FM][2];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int k = (c0 + u) * 64 + g * 16;
-      const bool kin0 = (c0 + u) < nk && k < K, kin1 = (c0 + u) < nk && k + 8 < K;
+      const int k = (c0 + u) * 64 + g * 8;
+      const bool kin0 = (c0 + u) < nk && k < K, kin1 = (c0 + u) < nk && k + 32 < K;
 #pragma unroll
       for (int f = 0; f < NF; ++f) {
         bb[u][f][0] = (b_ok[f] && kin0) ? __builtin_nontemporal_load((const u32x4_t*)(b_src[f] + (c0 + u) * 64))
                                         : u32x4_t{0, 0, 0, 0};
-        bb[u][f][1] = (b_ok[f] && kin1) ? __builtin_nontemporal_load((const u32x4_t*)(b_src[f] + (c0 + u) * 64 + 8))
+        bb[u][f][1] = (b_ok[f] && kin1) ? __builtin_nontemporal_load((const u32x4_t*)(b_src[f] + (c0 + u) * 64 + 32))
                                         : u32x4_t{0, 0, 0, 0};
       }
 #pragma unroll
       for (int fm = 0; fm < FM; ++fm) {
         aa[u][fm][0] = (a_ok[fm] && kin0) ? *(const u32x4_t*)(a_src[fm] + (c0 + u) * 64) : u32x4_t{0, 0, 0, 0};
-        aa[u][fm][1] = (a_ok[fm] && kin1) ? *(const u32x4_t*)(a_src[fm] + (c0 + u) * 64 + 8) : u32x4_t{0, 0, 0, 0};
+        aa[u][fm][1] = (a_ok[fm] && kin1) ? *(const u32x4_t*)(a_src[fm] + (c0 + u) * 64 + 32) : u32x4_t{0, 0, 0, 0};
       }
     }
 #pragma unroll
@@ -478,14 +404,14 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void grouped_lds8(GroupArgs 
     i32x8_t af[FM], bfr[FN];
 #pragma unroll
     for (int fm = 0; fm < FM; ++fm) {
-      const u8* src = &As[buf][(wm * WM + fm * 16 + r) * LDK8 + g * 32];
-      u32x4_t lo = *(const u32x4_t*)src, hi = *(const u32x4_t*)(src + 16);
+      const u8* src = &As[buf][(wm * WM + fm * 16 + r) * LDK8 + g * 16];
+      u32x4_t lo = *(const u32x4_t*)src, hi = *(const u32x4_t*)(src + 64);
       af[fm] = i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
     }
 #pragma unroll
     for (int fn = 0; fn < FN; ++fn) {
-      const u8* src = &Bs[buf][(brow[fn] + r) * LDK8 + g * 32];
-      u32x4_t lo = *(const u32x4_t*)src, hi = *(const u32x4_t*)(src + 16);
+      const u8* src = &Bs[buf][(brow[fn] + r) * LDK8 + g * 16];
+      u32x4_t lo = *(const u32x4_t*)src, hi = *(const u32x4_t*)(src + 64);
       bfr[fn] = i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
     }
 #pragma unroll
@@ -508,7 +434,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void grouped_lds8(GroupArgs 
       for (int fn = 0; fn < FN; ++fn) {
         const int col = pn * BN + wn * WN + fn * 16 + r;
         const bool ok = col < p.N;
-        store_frag<OutT, ACT, __bf16>(p, s_pairs, row0, col, acc[fm][fn], acc[fm][fn],
+        store_frag<OutT, ACT, typename OutRound<OutT>::type>(p, s_pairs, row0, col, acc[fm][fn], acc[fm][fn],
                                       ok ? ws[col] : 0.f, 0.f, rs, ok);
       }
     } else {
@@ -516,7 +442,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void grouped_lds8(GroupArgs 
       for (int fn = 0; fn < FN / 2; ++fn) {
         const int col = pn * (BN / 2) + wn * (WN / 2) + fn * 16 + r;
         const bool ok = col < half;
-        store_frag<OutT, ACT, __bf16>(p, s_pairs, row0, col, acc[fm][fn], acc[fm][fn + FN / 2],
+        store_frag<OutT, ACT, typename OutRound<OutT>::type>(p, s_pairs, row0, col, acc[fm][fn], acc[fm][fn + FN / 2],
                                       ok ? ws[col] : 0.f, ok ? ws[col + half] : 0.f, rs, ok);
       }
     }
@@ -553,7 +479,7 @@ __global__ __launch_bounds__(256) void grouped_stream8(GroupArgs p) {
     int pair = s_pairs[fm * 16 + r];
     a_ok[fm] = pair < p.n_pairs;
     long long src = p.by_token ? pair / p.topk : pair;
-    a_src[fm] = A + (a_ok[fm] ? src * p.sa : 0) + g * 32;
+    a_src[fm] = A + (a_ok[fm] ? src * p.sa : 0) + g * 16;
   }
   const u8* b_src[NF];
   bool b_ok[NF];
@@ -573,7 +499,7 @@ __global__ __launch_bounds__(256) void grouped_stream8(GroupArgs p) {
       n = f < H2 ? c : c + half;
       colv[f] = c;
     }
-    b_src[f] = B + (b_ok[f] ? n * p.sbn : 0) + g * 32;
+    b_src[f] = B + (b_ok[f] ? n * p.sbn : 0) + g * 16;
   }
 
   f32x4_t acc[FM][NF];
@@ -587,19 +513,19 @@ __global__ __launch_bounds__(256) void grouped_stream8(GroupArgs p) {
     u32x4_t bb[U][NF][2], aa[U][FM][2];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int k = (c0 + u) * 128 + g * 32;
-      const bool kin0 = (c0 + u) < nk && k < K, kin1 = (c0 + u) < nk && k + 16 < K;
+      const int k = (c0 + u) * 128 + g * 16;
+      const bool kin0 = (c0 + u) < nk && k < K, kin1 = (c0 + u) < nk && k + 64 < K;
 #pragma unroll
       for (int f = 0; f < NF; ++f) {
         bb[u][f][0] = (b_ok[f] && kin0) ? __builtin_nontemporal_load((const u32x4_t*)(b_src[f] + (c0 + u) * 128))
                                         : u32x4_t{0, 0, 0, 0};
-        bb[u][f][1] = (b_ok[f] && kin1) ? __builtin_nontemporal_load((const u32x4_t*)(b_src[f] + (c0 + u) * 128 + 16))
+        bb[u][f][1] = (b_ok[f] && kin1) ? __builtin_nontemporal_load((const u32x4_t*)(b_src[f] + (c0 + u) * 128 + 64))
                                         : u32x4_t{0, 0, 0, 0};
       }
 #pragma unroll
       for (int fm = 0; fm < FM; ++fm) {
         aa[u][fm][0] = (a_ok[fm] && kin0) ? *(const u32x4_t*)(a_src[fm] + (c0 + u) * 128) : u32x4_t{0, 0, 0, 0};
-        aa[u][fm][1] = (a_ok[fm] && kin1) ? *(const u32x4_t*)(a_src[fm] + (c0 + u) * 128 + 16) : u32x4_t{0, 0, 0, 0};
+        aa[u][fm][1] = (a_ok[fm] && kin1) ? *(const u32x4_t*)(a_src[fm] + (c0 + u) * 128 + 64) : u32x4_t{0, 0, 0, 0};
       }
     }
 #pragma unroll
@@ -626,12 +552,12 @@ __global__ __launch_bounds__(256) void grouped_stream8(GroupArgs p) {
     if constexpr (ACT == ACT_NONE) {
 #pragma unroll
       for (int f = 0; f < NF; ++f)
-        store_frag<OutT, ACT, __bf16>(p, s_pairs, fm * 16, colv[f], acc[fm][f], acc[fm][f],
+        store_frag<OutT, ACT, typename OutRound<OutT>::type>(p, s_pairs, fm * 16, colv[f], acc[fm][f], acc[fm][f],
                                       b_ok[f] ? ws[colv[f]] : 0.f, 0.f, rs, b_ok[f]);
     } else {
 #pragma unroll
       for (int f = 0; f < NF / 2; ++f)
-        store_frag<OutT, ACT, __bf16>(p, s_pairs, fm * 16, colv[f], acc[fm][f], acc[fm][f + NF / 2],
+        store_frag<OutT, ACT, typename OutRound<OutT>::type>(p, s_pairs, fm * 16, colv[f], acc[fm][f], acc[fm][f + NF / 2],
                                       b_ok[f] ? ws[colv[f]] : 0.f, b_ok[f] ? ws[colv[f] + half] : 0.f,
                                       rs, b_ok[f]);
     }
@@ -643,6 +569,16 @@ __global__ __launch_bounds__(256) void grouped_stream8(GroupArgs p) {
 // ---------------------------------------------------------------------------------------------------
 // Compiled tiles: bm 16/32 -> stream kernels (4 waves x NF fragments); bm 64/128 -> LDS kernels.
 constexpr int STREAM_NF = 2;  // 16-row weight fragments per wave
+
+// FLIDE_MOE_LEGACY_LDS=1 selects the register-staged LDS kernels instead of the direct-to-LDS ones
+// for 64/128-row tiles (same arithmetic and bits; kept for comparison).
+bool legacy_lds() {
+  static const bool v = [] {
+    const char* s = getenv("FLIDE_MOE_LEGACY_LDS");
+    return s && s[0] == '1';
+  }();
+  return v;
+}
 constexpr int STREAM_U = 4;   // K chunks in flight per wave
 
 template <typename T, typename OutT, int ACT>
@@ -657,6 +593,12 @@ int launch16(GroupArgs& p, int bm, hipStream_t st) {
     if (bm == 16) grouped_stream16<T, OutT, ACT, 1, STREAM_NF, STREAM_U><<<grid, block, 0, st>>>(p);
     else grouped_stream16<T, OutT, ACT, 2, STREAM_NF, STREAM_U><<<grid, block, 0, st>>>(p);
     return FLIDE_MOE_OK;
+  }
+  if ((bm == 64 || bm == 128 || bm == 256) && !legacy_lds()) {
+    const int out_dtype = std::is_same<OutT, float>::value ? FLIDE_F32
+                          : std::is_same<OutT, Bf16Out>::value ? FLIDE_BF16 : FLIDE_F16;
+    const int rc = dma_dispatch16(p, std::is_same<T, __bf16>::value, out_dtype, ACT, bm, st);
+    if (rc != FLIDE_MOE_ERR_TILE) return rc;   // else K is too short for the ring: the LDS kernel below
   }
   if (bm == 64 || bm == 128) {
     constexpr int BN = 128;
@@ -683,6 +625,12 @@ int launch8(GroupArgs& p, int bm, hipStream_t st) {
     if (bm == 16) grouped_stream8<OutT, ACT, 1, STREAM_NF, STREAM_U><<<grid, block, 0, st>>>(p);
     else grouped_stream8<OutT, ACT, 2, STREAM_NF, STREAM_U><<<grid, block, 0, st>>>(p);
     return FLIDE_MOE_OK;
+  }
+  if ((bm == 64 || bm == 128 || bm == 256) && !legacy_lds()) {
+    const int out_dtype = std::is_same<OutT, float>::value ? FLIDE_F32
+                          : std::is_same<OutT, Bf16Out>::value ? FLIDE_BF16 : FLIDE_F16;
+    const int rc = dma_dispatch8(p, out_dtype, ACT, bm, st);
+    if (rc != FLIDE_MOE_ERR_TILE) return rc;   // else K is too short for the ring: the LDS kernel below
   }
   if (bm == 64 || bm == 128) {
     constexpr int BN = 128;

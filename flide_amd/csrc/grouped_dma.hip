@@ -1,0 +1,405 @@
+// Prefill-shaped grouped products: direct-to-LDS loads, a multi-stage ring and large MFMA tiles.
+//
+// One workgroup (4 waves, one per SIMD) computes a BM-row block of pairs (one expert, as align padded
+// it) against a BN-row tile of that expert's weight. Per K stage it moves (BM + BN) rows of 128 bytes
+// straight from global memory into LDS with global_load_lds_dwordx4 (gfx950): no VGPR staging, no LDS
+// write instructions. NS stages are in flight: while the MFMAs consume stage kt, the loads of stages
+// kt+1 .. kt+NS-1 are outstanding; a wave waits only for its own loads of stage kt (vmcnt) and one
+// barrier per stage publishes everyone's.
+//
+// LDS layout: rows of 8 x 16-byte chunks, chunk c of row r stored at position c ^ (r & 7). Measured on
+// gfx950 (SQ_LDS_BANK_CONFLICT), this makes every MFMA operand read here conflict-free: a 16-row
+// fragment read of chunk c (16-bit steps: c = s*4 + g; float8: c = g and g + 4) runs at the full
+// 256 bytes per clock, where unswizzled rows or chunk pairs (2g, 2g + 1) take twice as long.
+// A direct load writes 64 lanes x 16 bytes contiguously, so each lane fetches the global chunk that
+// belongs at its LDS position under that swizzle.
+//
+// Padding rows (the sentinel pair) and weight rows past N load real but unused data (row 0 / the last
+// valid row): MFMA rows and columns never mix, and the epilogue stores neither. K tails read a 16-byte
+// block of zeros. Work items are ordered so each XCD (workgroup b runs on XCD b % 8) walks a contiguous
+// range of (block, column tile) items: the block's rows and the expert's weight tiles are reused from
+// that XCD's L2.
+//
+// Arithmetic is the same as every other grouped kernel here (common.hpp): 16-bit products in 32-wide
+// K steps with lane group g holding k = c*32 + g*8 + [0, 8); float8 in 128-wide steps with lane group g
+// holding k = g*16 + [0, 16) and 64 + g*16 + [0, 16).
+#include "grouped_common.hpp"
+
+#define FLIDE_GLOBAL_AS __attribute__((address_space(1)))
+#define FLIDE_LDS_AS __attribute__((address_space(3)))
+
+namespace {
+using namespace grouped_detail;
+
+__device__ __attribute__((aligned(16))) const uint32_t g_zero16[4] = {0, 0, 0, 0};
+
+template <int N> FLIDE_DEV void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  // s_waitcnt: vmcnt[3:0] bits 3:0, vmcnt[5:4] bits 15:14; expcnt (6:4) and lgkmcnt (11:8) left open
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+FLIDE_DEV void dma16(const void* src, FLIDE_LDS_AS void* dst) {
+  __builtin_amdgcn_global_load_lds((const FLIDE_GLOBAL_AS void*)src, dst, 16, 0, 0);
+}
+
+// chunk swizzle of a row with CPR 16-byte chunks (8 for 128-byte rows, 4 for 64-byte rows); both
+// measured bank-conflict-free for the fragment reads below
+template <int CPR> FLIDE_DEV int swz(int row) { return CPR == 8 ? (row & 7) : ((row >> 1) & 3); }
+
+// Waits until at most `ahead` stages of this wave's loads are still in flight (each stage = L loads).
+template <int NS, int L> FLIDE_DEV void wait_stage(int ahead) {
+  static_assert(NS >= 2 && NS <= 4, "stage ring of 2..4");
+  if constexpr (NS == 2) {
+    wait_vmcnt<0>();
+  } else if constexpr (NS == 3) {
+    if (ahead >= 1) wait_vmcnt<L>(); else wait_vmcnt<0>();
+  } else {
+    if (ahead >= 2) wait_vmcnt<2 * L>(); else if (ahead == 1) wait_vmcnt<L>(); else wait_vmcnt<0>();
+  }
+}
+
+// Element type traits of the two kernel families: 16-bit (2 bytes, 64 K per 128-byte stage row, two
+// 32-wide MFMA steps) and float8 (1 byte, 128 K per stage row, one 128-wide MFMA step).
+template <typename T> struct DmaElem {
+  static constexpr int BYTES = 2;
+};
+struct Fp8Tag {};
+template <> struct DmaElem<Fp8Tag> {
+  static constexpr int BYTES = 1;
+};
+
+template <typename T, typename OutT, int ACT, int BM, int BN, int WAVES_M, int WAVES_N, int NS, int ROWB, int OCC,
+          int XCD_CHUNK_BLOCKS>
+__global__ __launch_bounds__(256, OCC) void grouped_dma(GroupArgs p) {
+  constexpr bool FP8 = std::is_same<T, Fp8Tag>::value;
+  constexpr int EB = DmaElem<T>::BYTES;
+  constexpr int KS = ROWB / EB;                // K values per stage
+  constexpr int CPR = ROWB / 16;               // 16-byte chunks per stage row
+  constexpr int RPI = 64 / CPR;                // rows one 1 KB load instruction fills
+  constexpr int STEPS = FP8 ? 1 : ROWB / 64;   // MFMA K steps per stage
+  constexpr int A_BYTES = BM * ROWB, B_BYTES = BN * ROWB, STAGE = A_BYTES + B_BYTES;
+  constexpr int LA = BM / (4 * RPI), LB = BN / (4 * RPI);   // 1 KB loads per wave per stage
+  static_assert(!FP8 || ROWB == 128, "float8 stages hold one 128-wide MFMA step");
+  static_assert(BM % (4 * RPI) == 0 && BN % (4 * RPI) == 0, "tile rows split over 4 waves");
+  constexpr int L = LA + LB;
+  constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
+  constexpr int FM = WM / 16, FN = WN / 16;
+  static_assert(WAVES_M * WAVES_N == 4, "4 waves");
+  static_assert(BM % 32 == 0 && BN % 32 == 0, "tile rows come in 32s");
+  static_assert(ACT == ACT_NONE || FN % 2 == 0, "gated tiles pair gate and up fragments");
+  static_assert((NS - 1) * L < 64, "loads in flight must fit vmcnt");
+
+  // one LDS object per ring slot: distinct objects let the compiler see that reading slot s does not
+  // alias the loads still landing in the other slots (it would otherwise wait for all of them)
+  __shared__ __attribute__((aligned(1024))) char lds0[STAGE];
+  __shared__ __attribute__((aligned(1024))) char lds1[STAGE];
+  __shared__ __attribute__((aligned(1024))) char lds2[NS > 2 ? STAGE : 16];
+  __shared__ __attribute__((aligned(1024))) char lds3[NS > 3 ? STAGE : 16];
+  __shared__ int s_pairs[BM];
+  __shared__ float s_ascale[FP8 ? BM : 1];
+
+  const int tid = threadIdx.x, l = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform, in an SGPR
+  // Workgroup b runs on XCD b % 8. Items (block, column tile) are cut into chunks of CH items (a few
+  // blocks of one expert and all their column tiles) and chunk c goes to XCD c % 8, so each XCD's
+  // workgroups reuse the chunk's rows and weight tiles from that XCD's L2, and the dead items at the
+  // end of the static grid spread over all XCDs. The host rounds the grid to a multiple of 8 * CH.
+  const int CH = p.ntn * XCD_CHUNK_BLOCKS;
+  const int b = blockIdx.x;
+  const int j = b >> 3;
+  const int widx = ((j / CH) * 8 + (b & 7)) * CH + j % CH;
+  const int pm = widx / p.ntn, pn = widx % p.ntn;
+  if (pm >= p.nbm || pm * BM >= *p.used) return;
+  const long long e = p.blocks[pm];
+  for (int r = tid; r < BM; r += 256) {
+    const int pair = p.rows[pm * BM + r];
+    s_pairs[r] = pair;
+    if constexpr (FP8) {
+      const long long src = p.by_token ? pair / p.topk : pair;
+      s_ascale[r] = pair < p.n_pairs ? p.a_scale[src] : 0.f;
+    }
+  }
+  __syncthreads();
+
+  const int K = p.K;
+  const int half = p.N / 2;
+  const char* A = (const char*)p.a;
+  const char* B = (const char*)p.w + e * p.sbe * EB;
+
+  // This lane's global source for each of its loads: tile row (instr * RPI + l / CPR) and logical chunk
+  // c = (l % CPR) ^ swz(row). Instruction rows start at multiples of RPI, so swz(row) and therefore c
+  // (and the chunk's K offset kc) depend on the lane only.
+  const int kc = ((l % CPR) ^ swz<CPR>(l / CPR)) * (16 / EB);
+  const char* a_src[LA];
+#pragma unroll
+  for (int i = 0; i < LA; ++i) {
+    const int row = (wave * LA + i) * RPI + l / CPR;
+    const int pair = s_pairs[row];
+    const long long src = pair < p.n_pairs ? (p.by_token ? pair / p.topk : pair) : 0;
+    a_src[i] = A + (src * p.sa + kc) * EB;
+  }
+  const char* b_src[LB];
+#pragma unroll
+  for (int i = 0; i < LB; ++i) {
+    const int row = (wave * LB + i) * RPI + l / CPR;
+    long long n;
+    if constexpr (ACT == ACT_NONE) {
+      n = (long long)pn * BN + row;
+      if (n >= p.N) n = p.N - 1;
+    } else {
+      int cc = pn * (BN / 2) + (row < BN / 2 ? row : row - BN / 2);
+      if (cc >= half) cc = half - 1;
+      n = row < BN / 2 ? cc : cc + half;
+    }
+    b_src[i] = B + (n * p.sbn + kc) * EB;
+  }
+
+  const int wm = wave % WAVES_M, wn = wave / WAVES_M;
+  const int r = l & 15, g = l >> 4;
+  // LDS byte offset of this lane's chunk j within a 16-row fragment (16-bit: logical chunk s*4 + g for
+  // MFMA step s; float8: chunks g and g + 4 of one step). Fragments start at multiples of 16 rows, so
+  // the swizzle depends on r only: a fragment at tile row R adds the constant R * ROWB.
+  int lane_off[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) lane_off[j] = r * ROWB + ((((j * 4 + g) % CPR) ^ swz<CPR>(r)) << 4);
+  auto a_off = [&](int fm, int j) { return (wm * WM + fm * 16) * ROWB + lane_off[j]; };
+  bool m_live[FM];
+#pragma unroll
+  for (int fm = 0; fm < FM; ++fm)   // a block's valid pairs come first: a fragment whose first row is padding is all padding
+    m_live[fm] = __builtin_amdgcn_readfirstlane(s_pairs[wm * WM + fm * 16]) < p.n_pairs;
+  int brow[FN], colbase[FN];
+#pragma unroll
+  for (int fn = 0; fn < FN; ++fn) {
+    if constexpr (ACT == ACT_NONE) {
+      brow[fn] = wn * WN + fn * 16;
+      colbase[fn] = pn * BN + brow[fn];
+    } else {
+      constexpr int H2 = FN / 2;
+      const int f = fn < H2 ? fn : fn - H2;
+      brow[fn] = (fn < H2 ? 0 : BN / 2) + wn * (WN / 2) + f * 16;
+      colbase[fn] = pn * (BN / 2) + wn * (WN / 2) + f * 16;
+    }
+  }
+  auto b_off = [&](int fn, int j) { return A_BYTES + brow[fn] * ROWB + lane_off[j]; };
+  const int ncols = ACT == ACT_NONE ? p.N : half;
+  const bool wave_live = __builtin_amdgcn_readfirstlane(colbase[0]) < ncols && m_live[0];
+
+  f32x4_t acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  // The K loop runs inside a lambda whose ring-slot pointers are __restrict__: after inlining, every
+  // LDS access carries alias-scope metadata, which lets the compiler's wait-count pass see that reading
+  // slot s does not alias the loads still landing in the other slots. The steady-state loop is also
+  // branch-free (unconditional loads, a constant wait count): control-flow joins make that pass fall
+  // back to waiting for every outstanding load before each LDS read, collapsing the ring to one stage.
+  const int nk = (K + KS - 1) / KS;
+  // FMA: fragment rows this block computes (all FM, or fewer when the waves span the whole block and
+  // its tail is padding: every wave then skips the same dead rows)
+  auto kloop = [&](auto fma_tag, char* __restrict__ s0, char* __restrict__ s1, char* __restrict__ s2,
+                   char* __restrict__ s3) {
+    constexpr int FMA = decltype(fma_tag)::value;
+    auto slot_ptr = [&](int slot) -> char* { return slot == 0 ? s0 : slot == 1 ? s1 : slot == 2 ? s2 : s3; };
+    // loads of stage kt into ring slot `slot`; K-tail chunks read zeros through a select, not a branch
+    auto issue = [&](int kt, int slot) {
+      FLIDE_LDS_AS char* sb = (FLIDE_LDS_AS char*)slot_ptr(slot);
+      const int k0 = kt * KS;
+      const long long kb = (long long)k0 * EB;
+#pragma unroll
+      for (int i = 0; i < LA; ++i) {
+        const void* src = (k0 + kc < K) ? (const void*)(a_src[i] + kb) : (const void*)g_zero16;
+        dma16(src, sb + (wave * LA + i) * 1024);
+      }
+#pragma unroll
+      for (int i = 0; i < LB; ++i) {
+        const void* src = (k0 + kc < K) ? (const void*)(b_src[i] + kb) : (const void*)g_zero16;
+        dma16(src, sb + A_BYTES + (wave * LB + i) * 1024);
+      }
+    };
+    auto compute = [&](int slot) {
+      const char* sbase = slot_ptr(slot);
+      if constexpr (FP8) {
+        i32x8_t af[FMA], bfr[FN];
+#pragma unroll
+        for (int fm = 0; fm < FMA; ++fm) {
+          const u32x4_t lo = *(const u32x4_t*)(sbase + a_off(fm, 0));
+          const u32x4_t hi = *(const u32x4_t*)(sbase + a_off(fm, 1));
+          af[fm] = i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+        }
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn) {
+          const u32x4_t lo = *(const u32x4_t*)(sbase + b_off(fn, 0));
+          const u32x4_t hi = *(const u32x4_t*)(sbase + b_off(fn, 1));
+          bfr[fn] = i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+        }
+#pragma unroll
+        for (int fm = 0; fm < FMA; ++fm)
+#pragma unroll
+          for (int fn = 0; fn < FN; ++fn) acc[fm][fn] = mfma_fp8(af[fm], bfr[fn], acc[fm][fn]);
+      } else {
+#pragma unroll
+        for (int s = 0; s < STEPS; ++s) {
+          u32x4_t af[FMA], bfr[FN];
+#pragma unroll
+          for (int fm = 0; fm < FMA; ++fm) af[fm] = *(const u32x4_t*)(sbase + a_off(fm, s));
+#pragma unroll
+          for (int fn = 0; fn < FN; ++fn) bfr[fn] = *(const u32x4_t*)(sbase + b_off(fn, s));
+#pragma unroll
+          for (int fm = 0; fm < FMA; ++fm)
+#pragma unroll
+            for (int fn = 0; fn < FN; ++fn) acc[fm][fn] = Mfma16<T>::mma(af[fm], bfr[fn], acc[fm][fn]);
+        }
+      }
+    };
+    // prologue: the host guarantees nk >= NS - 1, so these loads are unconditional (a conditional load
+    // here would again make the wait-count pass conservative at the loop header)
+#pragma unroll
+    for (int st = 0; st < NS - 1; ++st) issue(st, st);
+    // steady state: stage kt computes while stages kt+1 .. kt+NS-1 load
+    const int nmain = nk - (NS - 1);   // iterations that issue a load
+    int kt0 = 0;
+    for (; kt0 + NS <= nmain; kt0 += NS) {
+#pragma unroll
+      for (int slot = 0; slot < NS; ++slot) {
+        wait_stage<NS, L>(NS - 2);
+        __builtin_amdgcn_s_barrier();
+        issue(kt0 + slot + NS - 1, (slot + NS - 1) % NS);
+        compute(slot);
+      }
+    }
+    // drain: the remaining issuing iterations (fewer than NS) and the last NS - 1 stages
+#pragma unroll
+    for (int i = 0; i < 2 * NS - 2; ++i) {
+      const int kt = kt0 + i;
+      if (kt < nk) {
+        wait_stage<NS, L>(min(NS - 2, nk - 1 - kt));
+        __builtin_amdgcn_s_barrier();
+        if (kt + NS - 1 < nk) issue(kt + NS - 1, (i + NS - 1) % NS);
+        compute(i % NS);
+      }
+    }
+  };
+  if constexpr (WAVES_M == 1 && FM == 16) {
+    int nlive = 0;   // live fragment rows (a block's valid pairs come first)
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm) nlive += m_live[fm] ? 1 : 0;
+    if (nlive <= 4) kloop(std::integral_constant<int, 4>{}, lds0, lds1, lds2, lds3);
+    else if (nlive <= 8) kloop(std::integral_constant<int, 8>{}, lds0, lds1, lds2, lds3);
+    else if (nlive <= 12) kloop(std::integral_constant<int, 12>{}, lds0, lds1, lds2, lds3);
+    else kloop(std::integral_constant<int, 16>{}, lds0, lds1, lds2, lds3);
+  } else {
+    kloop(std::integral_constant<int, FM>{}, lds0, lds1, lds2, lds3);
+  }
+
+  if (!wave_live) return;
+
+  typedef typename std::conditional<FP8, typename OutRound<OutT>::type, T>::type RT;   // gu rounding
+  const float* ws = FP8 ? p.w_scale + e * p.sse : nullptr;
+#pragma unroll
+  for (int fm = 0; fm < FM; ++fm) {
+    if (!m_live[fm]) continue;
+    const int row0 = wm * WM + fm * 16;
+    float rs[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) rs[i] = FP8 ? s_ascale[row0 + g * 4 + i] : 1.f;
+    if constexpr (ACT == ACT_NONE) {
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn) {
+        const int col = colbase[fn] + r;
+        const bool ok = col < p.N;
+        store_frag<OutT, ACT, RT>(p, s_pairs, row0, col, acc[fm][fn], acc[fm][fn],
+                                  FP8 ? (ok ? ws[col] : 0.f) : 1.f, 1.f, rs, ok);
+      }
+    } else {
+#pragma unroll
+      for (int fn = 0; fn < FN / 2; ++fn) {
+        const int col = colbase[fn] + r;
+        const bool ok = col < half;
+        store_frag<OutT, ACT, RT>(p, s_pairs, row0, col, acc[fm][fn], acc[fm][fn + FN / 2],
+                                  FP8 ? (ok ? ws[col] : 0.f) : 1.f, FP8 ? (ok ? ws[col + half] : 0.f) : 1.f,
+                                  rs, ok);
+      }
+    }
+  }
+}
+
+// Tiles (B = 256 weight rows):
+//  bm 256 (16-bit): 1 x 4 waves of 256 x 64, 64-byte stage rows, 4 stages = 128 KB, one workgroup per CU;
+//     the waves share all 256 rows, so a block's padded tail costs no MFMA time
+//  bm 128 (16-bit): 2 x 2 waves of 64 x 128, 64-byte stage rows, 3 stages = 72 KB, two workgroups per CU
+//  bm 64  (16-bit): 1 x 4 waves of 64 x 64, 64-byte stage rows, 3 stages = 60 KB, two workgroups per CU
+//  float8: 128-byte stage rows (one 128-wide MFMA step); bm 256: 2 stages = 128 KB; bm 128/64: 3 stages
+constexpr int DMA_BN = 256;
+
+template <typename T, typename OutT, int ACT, int BM, int WM_, int WN_, int NS, int ROWB, int OCC, int XB>
+int launch_one(GroupArgs& p, hipStream_t st) {
+  constexpr int KS = ROWB / DmaElem<T>::BYTES;
+  if (p.K < (NS - 1) * KS) return FLIDE_MOE_ERR_TILE;   // the ring needs NS - 1 full stages
+  const int cols = ACT == ACT_NONE ? p.N : p.N / 2;
+  const int per = ACT == ACT_NONE ? DMA_BN : DMA_BN / 2;
+  p.ntn = (cols + per - 1) / per;
+  const int items = p.nbm * p.ntn;
+  const int round = 8 * p.ntn * XB;
+  dim3 grid((items + round - 1) / round * round), block(256);
+  grouped_dma<T, OutT, ACT, BM, DMA_BN, WM_, WN_, NS, ROWB, OCC, XB><<<grid, block, 0, st>>>(p);
+  return FLIDE_MOE_OK;
+}
+
+template <typename T, typename OutT, int ACT>
+int launch_dma(GroupArgs& p, int bm, hipStream_t st) {
+  constexpr bool FP8 = std::is_same<T, Fp8Tag>::value;
+  if constexpr (FP8) {
+    if (bm == 256) return launch_one<T, OutT, ACT, 256, 1, 4, 2, 128, 1, 2>(p, st);
+    if (bm == 128) return launch_one<T, OutT, ACT, 128, 2, 2, 3, 128, 1, 4>(p, st);
+    if (bm == 64) return launch_one<T, OutT, ACT, 64, 1, 4, 3, 128, 1, 8>(p, st);
+  } else {
+    if (bm == 256) return launch_one<T, OutT, ACT, 256, 1, 4, 4, 64, 1, 2>(p, st);
+    if (bm == 128) return launch_one<T, OutT, ACT, 128, 2, 2, 3, 64, 2, 4>(p, st);
+    if (bm == 64) return launch_one<T, OutT, ACT, 64, 1, 4, 3, 64, 2, 8>(p, st);
+  }
+  return FLIDE_MOE_ERR_TILE;
+}
+
+}  // namespace
+
+namespace grouped_detail {
+
+int dma_dispatch16(GroupArgs& p, bool is_bf16, int out_dtype, int act, int bm, hipStream_t st) {
+  if (is_bf16) {
+    if (act == ACT_NONE && out_dtype == FLIDE_F32) return launch_dma<__bf16, float, ACT_NONE>(p, bm, st);
+    if (out_dtype != FLIDE_BF16) return FLIDE_MOE_ERR_ARG;
+    if (act == ACT_NONE) return launch_dma<__bf16, Bf16Out, ACT_NONE>(p, bm, st);
+    if (act == ACT_GEGLU) return launch_dma<__bf16, Bf16Out, ACT_GEGLU>(p, bm, st);
+    if (act == ACT_SWIGLU) return launch_dma<__bf16, Bf16Out, ACT_SWIGLU>(p, bm, st);
+    return FLIDE_MOE_ERR_ARG;
+  }
+  if (act == ACT_NONE && out_dtype == FLIDE_F32) return launch_dma<_Float16, float, ACT_NONE>(p, bm, st);
+  if (out_dtype != FLIDE_F16) return FLIDE_MOE_ERR_ARG;
+  if (act == ACT_NONE) return launch_dma<_Float16, F16Out, ACT_NONE>(p, bm, st);
+  if (act == ACT_GEGLU) return launch_dma<_Float16, F16Out, ACT_GEGLU>(p, bm, st);
+  if (act == ACT_SWIGLU) return launch_dma<_Float16, F16Out, ACT_SWIGLU>(p, bm, st);
+  return FLIDE_MOE_ERR_ARG;
+}
+
+int dma_dispatch8(GroupArgs& p, int out_dtype, int act, int bm, hipStream_t st) {
+  if (act == ACT_NONE) {
+    if (out_dtype == FLIDE_F32) return launch_dma<Fp8Tag, float, ACT_NONE>(p, bm, st);
+    if (out_dtype == FLIDE_BF16) return launch_dma<Fp8Tag, Bf16Out, ACT_NONE>(p, bm, st);
+    if (out_dtype == FLIDE_F16) return launch_dma<Fp8Tag, F16Out, ACT_NONE>(p, bm, st);
+    return FLIDE_MOE_ERR_ARG;
+  }
+  if (out_dtype == FLIDE_BF16) {
+    if (act == ACT_GEGLU) return launch_dma<Fp8Tag, Bf16Out, ACT_GEGLU>(p, bm, st);
+    if (act == ACT_SWIGLU) return launch_dma<Fp8Tag, Bf16Out, ACT_SWIGLU>(p, bm, st);
+  }
+  if (out_dtype == FLIDE_F16) {
+    if (act == ACT_GEGLU) return launch_dma<Fp8Tag, F16Out, ACT_GEGLU>(p, bm, st);
+    if (act == ACT_SWIGLU) return launch_dma<Fp8Tag, F16Out, ACT_SWIGLU>(p, bm, st);
+  }
+  return FLIDE_MOE_ERR_ARG;
+}
+
+}  // namespace grouped_detail

@@ -40,16 +40,16 @@ __global__ __launch_bounds__(256) void router_kernel(const u16* __restrict__ x, 
 #pragma unroll
   for (int nb = 0; nb < 4; ++nb) acc[nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   for (int k0 = 0; k0 < H; k0 += 64) {
-    // this lane's 16 K-values of the chunk: k0 + g*16 .. +16 (two MFMA steps of 8)
-    const int kk = k0 + g * 16;
+    // this lane's K-values of the two 32-wide MFMA steps: k0 + s*32 + g*8 .. +8
+    const int kk = k0 + g * 8;
     u32x4_t a0 = {0, 0, 0, 0}, a1 = {0, 0, 0, 0};
     if (tvalid && kk < H) a0 = *(const u32x4_t*)(xp + kk);
-    if (tvalid && kk + 8 < H) a1 = *(const u32x4_t*)(xp + kk + 8);
+    if (tvalid && kk + 32 < H) a1 = *(const u32x4_t*)(xp + kk + 32);
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb) {
       u32x4_t b0 = {0, 0, 0, 0}, b1 = {0, 0, 0, 0};
       if (evalid[nb] && kk < H) b0 = *(const u32x4_t*)(wp[nb] + kk);
-      if (evalid[nb] && kk + 8 < H) b1 = *(const u32x4_t*)(wp[nb] + kk + 8);
+      if (evalid[nb] && kk + 32 < H) b1 = *(const u32x4_t*)(wp[nb] + kk + 32);
       acc[nb] = Mfma16<T>::mma(a0, b0, acc[nb]);
       acc[nb] = Mfma16<T>::mma(a1, b1, acc[nb]);
     }

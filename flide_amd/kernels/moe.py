@@ -33,13 +33,13 @@ BK8 = 128
 def tile(pairs: int, fp8: bool, device=None) -> tuple[int, int, int, int, int]:
     """(block rows, block columns, waves, stages, row blocks per group) for a layer of `pairs` pairs.
     Block rows are what `align` pads each expert to: 16 or 32 rows run the streaming (decode) kernels,
-    whose weights go from HBM straight into MFMA registers; 64 or 128 rows the LDS-tiled kernels. The
-    K order is the same for every tile, so the bits do not change with the choice."""
+    whose weights go from HBM straight into MFMA registers; 64, 128 or 256 rows the LDS-tiled kernels.
+    The K order is the same for every tile, so the bits do not change with the choice."""
     if pairs <= 2048:
         bm = 16
     elif pairs <= 8192:
         bm = 32
-    elif pairs <= 24576:
+    elif pairs <= 16384:
         bm = 64
     else:
         bm = 128

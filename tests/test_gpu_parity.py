@@ -116,7 +116,7 @@ def test_align_configs_exact(cfg):
 # --------------------------------------------------------------------------------------------------
 # grouped products and the experts
 # --------------------------------------------------------------------------------------------------
-@pytest.mark.parametrize("bm", [16, 32, 64, 128])
+@pytest.mark.parametrize("bm", [16, 32, 64, 128, 256])
 @pytest.mark.parametrize("by_token,mul_w,out32", [(True, False, False), (False, True, True)])
 def test_grouped_bf16(bm, by_token, mul_w, out32):
     print(f"grouped bm={bm} by_token={by_token}", flush=True)
@@ -170,8 +170,8 @@ def test_experts_cfg1_decode():
 
 
 def test_experts_cfg1_shape_other_tiles():
-    """T = 512 and 2048 at the Gemma shape run the bm 32 / 64 / 128 kernels."""
-    for T in (512, 2048, 4096):
+    """T = 512 .. 8192 at the Gemma shape run the bm 32 / 64 / 128 / 256 kernels."""
+    for T in (512, 2048, 4096, 8192):
         print(f"experts cfg1 T={T}", flush=True)
         sub = np.random.default_rng(T).choice(T * 8, 256, replace=False)
         got, ref, _ = _experts_case(1, T=T, pairs_subset=np.sort(sub))
