@@ -187,7 +187,8 @@ def _guess_act(act) -> int:
     if kind == "swiglu":
         return _hip.ACT_SWIGLU
     code = getattr(act, "__code__", None)
-    names = set(code.co_names) if code is not None else set()
+    # names the callable calls: globals (co_names) and closure variables (co_freevars)
+    names = set(code.co_names) | set(code.co_freevars) if code is not None else set()
     names.add(getattr(act, "__name__", ""))
     if names & {"_geglu", "geglu"}:
         return _hip.ACT_GEGLU
