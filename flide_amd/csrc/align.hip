@@ -3,6 +3,7 @@
 // The reference runs one program per expert, each scanning all n pairs (O(E n)). Here two launches do
 // O(n) work in total:
 //   align_count  chunk c of ALIGN_CHUNK pairs -> an LDS histogram -> hist[c][E] in the workspace
+//                (skipped when all pairs fit one chunk: align_place<true> then counts them itself)
 //   align_place  every chunk sums the histograms before it (and all of them, for the padded expert
 //                offsets), then places its pairs in pair order: each wave walks its quarter of the
 //                chunk 64 pairs at a time; lanes with the same expert find each other with log2(E+1)
@@ -36,6 +37,7 @@ __global__ __launch_bounds__(ALIGN_THREADS) void align_count(const int* __restri
   for (int e = threadIdx.x; e < E; e += ALIGN_THREADS) hist[(long long)blockIdx.x * E + e] = h[e];
 }
 
+template <bool FUSED>
 __global__ __launch_bounds__(ALIGN_THREADS) void align_place(const int* __restrict__ ids, int n, int E,
                                                              int bm, int nchunks,
                                                              const int* __restrict__ hist,
@@ -51,16 +53,36 @@ __global__ __launch_bounds__(ALIGN_THREADS) void align_place(const int* __restri
   const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63;
   const int c = blockIdx.x;
 
-  // per-expert totals and the share of earlier chunks
-  for (int e = tid; e < E; e += ALIGN_THREADS) {
-    int b = 0, tot = 0;
-    for (int j = 0; j < nchunks; ++j) {
-      int v = hist[(long long)j * E + e];
-      if (j < c) b += v;
-      tot += v;
+  const int cbase = c * ALIGN_CHUNK;
+  const int wbase = cbase + wave * ALIGN_PER_WAVE;
+  const int wend = min(n, wbase + ALIGN_PER_WAVE);
+  if constexpr (FUSED) {
+    // one chunk holds every pair: count them here (per wave, which the placement needs anyway)
+    for (int e = l; e < E; e += 64) wcur[wave][e] = 0;
+    __syncthreads();
+    for (int i = wbase + l; i < wend; i += 64) {
+      int e = ids[i];
+      if ((unsigned)e < (unsigned)E) atomicAdd(&wcur[wave][e], 1);
     }
-    before[e] = b;
-    cnt[e] = tot;
+    __syncthreads();
+    for (int e = tid; e < E; e += ALIGN_THREADS) {
+      int tot = 0;
+      for (int w = 0; w < ALIGN_WAVES; ++w) tot += wcur[w][e];
+      before[e] = 0;
+      cnt[e] = tot;
+    }
+  } else {
+    // per-expert totals and the share of earlier chunks
+    for (int e = tid; e < E; e += ALIGN_THREADS) {
+      int b = 0, tot = 0;
+      for (int j = 0; j < nchunks; ++j) {
+        int v = hist[(long long)j * E + e];
+        if (j < c) b += v;
+        tot += v;
+      }
+      before[e] = b;
+      cnt[e] = tot;
+    }
   }
   __syncthreads();
   // exclusive scan of the padded counts over experts: each thread owns a run of ceil(E / 256)
@@ -89,16 +111,15 @@ __global__ __launch_bounds__(ALIGN_THREADS) void align_place(const int* __restri
   __syncthreads();
 
   // each wave's quarter of the chunk: its own histogram first, so waves place in pair order
-  const int cbase = c * ALIGN_CHUNK;
-  const int wbase = cbase + wave * ALIGN_PER_WAVE;
-  const int wend = min(n, wbase + ALIGN_PER_WAVE);
-  for (int e = l; e < E; e += 64) wcur[wave][e] = 0;
-  __syncthreads();
-  for (int i = wbase + l; i < wend; i += 64) {
-    int e = ids[i];
-    if ((unsigned)e < (unsigned)E) atomicAdd(&wcur[wave][e], 1);
+  if constexpr (!FUSED) {
+    for (int e = l; e < E; e += 64) wcur[wave][e] = 0;
+    __syncthreads();
+    for (int i = wbase + l; i < wend; i += 64) {
+      int e = ids[i];
+      if ((unsigned)e < (unsigned)E) atomicAdd(&wcur[wave][e], 1);
+    }
+    __syncthreads();
   }
-  __syncthreads();
   // wcur[w][e] <- start[e] + before[e] + pairs of waves < w in this chunk
   for (int e = tid; e < E; e += ALIGN_THREADS) {
     int a = start[e] + before[e];
@@ -161,10 +182,15 @@ extern "C" int flide_moe_align(const int* ids, int n, int E, int bm, int* rows, 
   int nchunks = (n + ALIGN_CHUNK - 1) / ALIGN_CHUNK;
   if (nchunks == 0) nchunks = 1;
   int* hist = (int*)workspace;
+  if (nchunks == 1) {   // every pair in one chunk: one launch counts and places
+    align_place<true><<<1, ALIGN_THREADS, 0, st>>>(ids, n, E, bm, 1, hist, rows, blocks, used, counts);
+    FLIDE_CHECK_LAUNCH();
+    return FLIDE_MOE_OK;
+  }
   align_count<<<nchunks, ALIGN_THREADS, 0, st>>>(ids, n, E, hist);
   FLIDE_CHECK_LAUNCH();
-  align_place<<<nchunks, ALIGN_THREADS, 0, st>>>(ids, n, E, bm, nchunks, hist, rows, blocks, used,
-                                                 counts);
+  align_place<false><<<nchunks, ALIGN_THREADS, 0, st>>>(ids, n, E, bm, nchunks, hist, rows, blocks, used,
+                                                        counts);
   FLIDE_CHECK_LAUNCH();
   return FLIDE_MOE_OK;
 }

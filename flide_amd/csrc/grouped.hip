@@ -23,6 +23,14 @@
 
 #include "grouped_common.hpp"
 
+// weight loads of the streaming kernels: ordinary loads measured faster than non-temporal ones on
+// MI355X for this pattern (5.6 vs 4.75 TB/s at the decode shape)
+#ifdef FLIDE_STREAM_NT_LOADS
+#define FLIDE_WLOAD(p) __builtin_nontemporal_load(p)
+#else
+#define FLIDE_WLOAD(p) (*(p))
+#endif
+
 namespace {
 using namespace grouped_detail;
 
@@ -188,27 +196,18 @@ __global__ __launch_bounds__(256) void grouped_stream16(GroupArgs p) {
   constexpr int BM = FM * 16;
   constexpr int BNW = 4 * NF * 16;  // weight rows per workgroup
   __shared__ int s_pairs[BM];
-  const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63;
+  const int tid = threadIdx.x, l = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int pm = blockIdx.x / p.ntn, pn = blockIdx.x % p.ntn;
-  if (pm * BM >= *p.used) return;
+  // `used` and the block's expert load together; the weight stream starts before the block's pair ids
+  // are known, so their latency overlaps the first weight loads
+  const int used = *p.used;
   const long long e = p.blocks[pm];
-  if (tid < BM) s_pairs[tid] = p.rows[pm * BM + tid];
-  __syncthreads();
+  if (pm * BM >= used) return;
 
   const int r = l & 15, g = l >> 4;
   const int K = p.K, half = p.N / 2;
-  const u16* A = (const u16*)p.a;
   const u16* B = (const u16*)p.w + e * p.sbe;
-
-  const u16* a_src[FM];
-  bool a_ok[FM];
-#pragma unroll
-  for (int fm = 0; fm < FM; ++fm) {
-    int pair = s_pairs[fm * 16 + r];
-    a_ok[fm] = pair < p.n_pairs;
-    long long src = p.by_token ? pair / p.topk : pair;
-    a_src[fm] = A + (a_ok[fm] ? src * p.sa : 0) + g * 8;
-  }
   const u16* b_src[NF];
   bool b_ok[NF];
   int colv[NF];
@@ -229,6 +228,36 @@ __global__ __launch_bounds__(256) void grouped_stream16(GroupArgs p) {
     }
     b_src[f] = B + (b_ok[f] ? n * p.sbn : 0) + g * 8;
   }
+  const int nk = (K + 63) / 64;
+  // weight chunks of one group of U 64-wide K chunks: [u][frag][MFMA step]
+  auto load_w = [&](int c0, u32x4_t (&bb)[U][NF][2]) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int k = (c0 + u) * 64 + g * 8;
+      const bool kin0 = (c0 + u) < nk && k < K, kin1 = (c0 + u) < nk && k + 32 < K;
+#pragma unroll
+      for (int f = 0; f < NF; ++f) {
+        bb[u][f][0] = (b_ok[f] && kin0) ? FLIDE_WLOAD((const u32x4_t*)(b_src[f] + (c0 + u) * 64)) : u32x4_t{0, 0, 0, 0};
+        bb[u][f][1] = (b_ok[f] && kin1) ? FLIDE_WLOAD((const u32x4_t*)(b_src[f] + (c0 + u) * 64 + 32))
+                                        : u32x4_t{0, 0, 0, 0};
+      }
+    }
+  };
+  u32x4_t bb[U][NF][2];
+  load_w(0, bb);
+
+  // the block's pair ids: straight from global for the operand rows, through LDS for the epilogue
+  const u16* A = (const u16*)p.a;
+  const u16* a_src[FM];
+  bool a_ok[FM];
+#pragma unroll
+  for (int fm = 0; fm < FM; ++fm) {
+    const int pair = p.rows[pm * BM + fm * 16 + r];
+    a_ok[fm] = pair < p.n_pairs;
+    const long long src = p.by_token ? pair / p.topk : pair;
+    a_src[fm] = A + (a_ok[fm] ? src * p.sa : 0) + g * 8;
+  }
+  if (tid < BM) s_pairs[tid] = p.rows[pm * BM + tid];
 
   f32x4_t acc[FM][NF];
 #pragma unroll
@@ -236,26 +265,21 @@ __global__ __launch_bounds__(256) void grouped_stream16(GroupArgs p) {
 #pragma unroll
     for (int j = 0; j < NF; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  const int nk = (K + 63) / 64;
   for (int c0 = 0; c0 < nk; c0 += U) {
-    u32x4_t bb[U][NF][2], aa[U][FM][2];
+    u32x4_t aa[U][FM][2];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int k = (c0 + u) * 64 + g * 8;
       const bool kin0 = (c0 + u) < nk && k < K, kin1 = (c0 + u) < nk && k + 32 < K;
-#pragma unroll
-      for (int f = 0; f < NF; ++f) {
-        bb[u][f][0] = (b_ok[f] && kin0) ? __builtin_nontemporal_load((const u32x4_t*)(b_src[f] + (c0 + u) * 64))
-                                        : u32x4_t{0, 0, 0, 0};
-        bb[u][f][1] = (b_ok[f] && kin1) ? __builtin_nontemporal_load((const u32x4_t*)(b_src[f] + (c0 + u) * 64 + 32))
-                                        : u32x4_t{0, 0, 0, 0};
-      }
 #pragma unroll
       for (int fm = 0; fm < FM; ++fm) {
         aa[u][fm][0] = (a_ok[fm] && kin0) ? *(const u32x4_t*)(a_src[fm] + (c0 + u) * 64) : u32x4_t{0, 0, 0, 0};
         aa[u][fm][1] = (a_ok[fm] && kin1) ? *(const u32x4_t*)(a_src[fm] + (c0 + u) * 64 + 32) : u32x4_t{0, 0, 0, 0};
       }
     }
+    // the next group's weights go out before this group's MFMAs
+    u32x4_t nb[U][NF][2];
+    if (c0 + U < nk) load_w(c0 + U, nb);
 #pragma unroll
     for (int u = 0; u < U; ++u)
 #pragma unroll
@@ -264,7 +288,17 @@ __global__ __launch_bounds__(256) void grouped_stream16(GroupArgs p) {
         for (int fm = 0; fm < FM; ++fm)
 #pragma unroll
           for (int f = 0; f < NF; ++f) acc[fm][f] = Mfma16<T>::mma(aa[u][fm][s], bb[u][f][s], acc[fm][f]);
+    if (c0 + U < nk) {
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int f = 0; f < NF; ++f) {
+          bb[u][f][0] = nb[u][f][0];
+          bb[u][f][1] = nb[u][f][1];
+        }
+    }
   }
+  __syncthreads();   // s_pairs for the epilogue
 
   const float ones[4] = {1.f, 1.f, 1.f, 1.f};
 #pragma unroll
@@ -568,7 +602,17 @@ __global__ __launch_bounds__(256) void grouped_stream8(GroupArgs p) {
 // dispatch
 // ---------------------------------------------------------------------------------------------------
 // Compiled tiles: bm 16/32 -> stream kernels (4 waves x NF fragments); bm 64/128 -> LDS kernels.
-constexpr int STREAM_NF = 2;  // 16-row weight fragments per wave
+#ifndef FLIDE_STREAM_NF
+#define FLIDE_STREAM_NF 2
+#endif
+#ifndef FLIDE_STREAM_U
+#define FLIDE_STREAM_U 4
+#endif
+#ifndef FLIDE_STREAM_NF_DOWN
+#define FLIDE_STREAM_NF_DOWN 2
+#endif
+constexpr int STREAM_NF = FLIDE_STREAM_NF;  // 16-row weight fragments per wave (gated products)
+constexpr int STREAM_NF_DOWN = FLIDE_STREAM_NF_DOWN;  // ... and for the plain (down) products
 
 // FLIDE_MOE_LEGACY_LDS=1 selects the register-staged LDS kernels instead of the direct-to-LDS ones
 // for 64/128-row tiles (same arithmetic and bits; kept for comparison).
@@ -579,19 +623,20 @@ bool legacy_lds() {
   }();
   return v;
 }
-constexpr int STREAM_U = 4;   // K chunks in flight per wave
+constexpr int STREAM_U = FLIDE_STREAM_U;   // K chunks in flight per wave
 
 template <typename T, typename OutT, int ACT>
 int launch16(GroupArgs& p, int bm, hipStream_t st) {
   dim3 block(256);
   if (bm == 16 || bm == 32) {
-    constexpr int BNW = 4 * STREAM_NF * 16;
+    constexpr int NF = ACT == ACT_NONE ? STREAM_NF_DOWN : STREAM_NF;
+    constexpr int BNW = 4 * NF * 16;
     const int cols = ACT == ACT_NONE ? p.N : p.N / 2;
     const int per = ACT == ACT_NONE ? BNW : BNW / 2;
     p.ntn = (cols + per - 1) / per;
     dim3 grid(p.nbm * p.ntn);
-    if (bm == 16) grouped_stream16<T, OutT, ACT, 1, STREAM_NF, STREAM_U><<<grid, block, 0, st>>>(p);
-    else grouped_stream16<T, OutT, ACT, 2, STREAM_NF, STREAM_U><<<grid, block, 0, st>>>(p);
+    if (bm == 16) grouped_stream16<T, OutT, ACT, 1, NF, STREAM_U><<<grid, block, 0, st>>>(p);
+    else grouped_stream16<T, OutT, ACT, 2, NF, STREAM_U><<<grid, block, 0, st>>>(p);
     return FLIDE_MOE_OK;
   }
   if ((bm == 64 || bm == 128 || bm == 256) && !legacy_lds()) {
@@ -617,13 +662,14 @@ template <typename OutT, int ACT>
 int launch8(GroupArgs& p, int bm, hipStream_t st) {
   dim3 block(256);
   if (bm == 16 || bm == 32) {
-    constexpr int BNW = 4 * STREAM_NF * 16;
+    constexpr int NF = ACT == ACT_NONE ? STREAM_NF_DOWN : STREAM_NF;
+    constexpr int BNW = 4 * NF * 16;
     const int cols = ACT == ACT_NONE ? p.N : p.N / 2;
     const int per = ACT == ACT_NONE ? BNW : BNW / 2;
     p.ntn = (cols + per - 1) / per;
     dim3 grid(p.nbm * p.ntn);
-    if (bm == 16) grouped_stream8<OutT, ACT, 1, STREAM_NF, STREAM_U><<<grid, block, 0, st>>>(p);
-    else grouped_stream8<OutT, ACT, 2, STREAM_NF, STREAM_U><<<grid, block, 0, st>>>(p);
+    if (bm == 16) grouped_stream8<OutT, ACT, 1, NF, STREAM_U><<<grid, block, 0, st>>>(p);
+    else grouped_stream8<OutT, ACT, 2, NF, STREAM_U><<<grid, block, 0, st>>>(p);
     return FLIDE_MOE_OK;
   }
   if ((bm == 64 || bm == 128 || bm == 256) && !legacy_lds()) {

@@ -5,6 +5,8 @@
 // One workgroup of 256 threads per row for the reductions. Rows are read with 16-byte vector loads
 // when the row length and stride allow it (every Gemma/Qwen shape does), else element by element.
 // All arithmetic is float32, rounded once at the store.
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace {
@@ -111,6 +113,71 @@ __global__ __launch_bounds__(RW_THREADS) void combine_norm_kernel(const void* __
   }
 }
 
+// combine_norm, vectorised for the common dtypes (y f32 or bf16; dense, out, w1, w2 bf16) and
+// H <= 4096: every load of the token (k rows of y, dense, both weights) is issued before any sum.
+template <typename YT, int KMAX>
+__global__ __launch_bounds__(RW_THREADS) void combine_norm_bf16_kernel(const YT* __restrict__ y,
+                                                                       const u16* __restrict__ dense,
+                                                                       long long sd, const u16* __restrict__ w1,
+                                                                       const u16* __restrict__ w2,
+                                                                       u16* __restrict__ out, long long so,
+                                                                       int H, int k, float eps) {
+  constexpr int V = 4;  // float4 groups per thread: H <= 256 * 4 * 4
+  __shared__ float red[4];
+  const long long t = blockIdx.x;
+  const int nv = H / 4;
+  float4 acc[V], dv[V];
+  float ss = 0.f, dd = 0.f;
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    const int c4 = threadIdx.x + v * RW_THREADS;
+    acc[v] = make_float4(0.f, 0.f, 0.f, 0.f);
+    dv[v] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (c4 >= nv) continue;
+    const uint2 draw = ((const uint2*)(dense + t * sd))[c4];
+    dv[v] = make_float4(bf16_to_f32(draw.x & 0xffff), bf16_to_f32(draw.x >> 16), bf16_to_f32(draw.y & 0xffff),
+                        bf16_to_f32(draw.y >> 16));
+    float4 yv[KMAX];
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j) {
+      if (j >= k) break;
+      const long long row = (t * k + j) * (long long)H;
+      if constexpr (std::is_same<YT, float>::value) {
+        yv[j] = ((const float4*)(y + row))[c4];
+      } else {
+        const uint2 raw = ((const uint2*)(y + row))[c4];
+        yv[j] = make_float4(bf16_to_f32(raw.x & 0xffff), bf16_to_f32(raw.x >> 16), bf16_to_f32(raw.y & 0xffff),
+                            bf16_to_f32(raw.y >> 16));
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j) {   // slot order
+      if (j >= k) break;
+      acc[v].x += yv[j].x; acc[v].y += yv[j].y; acc[v].z += yv[j].z; acc[v].w += yv[j].w;
+    }
+    ss += acc[v].x * acc[v].x + acc[v].y * acc[v].y + acc[v].z * acc[v].z + acc[v].w * acc[v].w;
+    dd += dv[v].x * dv[v].x + dv[v].y * dv[v].y + dv[v].z * dv[v].z + dv[v].w * dv[v].w;
+  }
+  const float sum_ss = block_sum(ss, red);
+  const float sum_dd = block_sum(dd, red);
+  const float inv_b = rsqrtf(sum_ss / H + eps);
+  const float inv_a = rsqrtf(sum_dd / H + eps);
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    const int c4 = threadIdx.x + v * RW_THREADS;
+    if (c4 >= nv) continue;
+    const uint2 a1 = ((const uint2*)w1)[c4], a2 = ((const uint2*)w2)[c4];
+    const float o0 = dv[v].x * inv_a * bf16_to_f32(a1.x & 0xffff) + acc[v].x * inv_b * bf16_to_f32(a2.x & 0xffff);
+    const float o1 = dv[v].y * inv_a * bf16_to_f32(a1.x >> 16) + acc[v].y * inv_b * bf16_to_f32(a2.x >> 16);
+    const float o2 = dv[v].z * inv_a * bf16_to_f32(a1.y & 0xffff) + acc[v].z * inv_b * bf16_to_f32(a2.y & 0xffff);
+    const float o3 = dv[v].w * inv_a * bf16_to_f32(a1.y >> 16) + acc[v].w * inv_b * bf16_to_f32(a2.y >> 16);
+    uint2 o;
+    o.x = (uint32_t)f32_to_bf16(o0) | ((uint32_t)f32_to_bf16(o1) << 16);
+    o.y = (uint32_t)f32_to_bf16(o2) | ((uint32_t)f32_to_bf16(o3) << 16);
+    ((uint2*)(out + t * so))[c4] = o;
+  }
+}
+
 // combine (Qwen): sum of the k rows + shared * sigmoid(gate); one workgroup per (token, 1024 columns)
 template <int YDT>
 __global__ __launch_bounds__(RW_THREADS) void combine_kernel(const void* __restrict__ y,
@@ -205,6 +272,22 @@ extern "C" int flide_moe_combine_norm(const void* y, int y_dtype, const void* de
   if ((uintptr_t)y & 15) return FLIDE_MOE_ERR_ARG;
   if (T == 0) return FLIDE_MOE_OK;
   hipStream_t st = (hipStream_t)stream;
+  const bool vec = out_dtype == FLIDE_BF16 && w_dtype == FLIDE_BF16 && H <= 4 * 4 * RW_THREADS && k <= 8 &&
+                   sd % 4 == 0 && so % 4 == 0 && !(((uintptr_t)dense | (uintptr_t)out | (uintptr_t)w1 | (uintptr_t)w2) & 7);
+  if (vec && y_dtype == FLIDE_F32) {
+    combine_norm_bf16_kernel<float, 8><<<T, RW_THREADS, 0, st>>>((const float*)y, (const u16*)dense, sd,
+                                                                 (const u16*)w1, (const u16*)w2, (u16*)out, so,
+                                                                 H, k, eps);
+    FLIDE_CHECK_LAUNCH();
+    return FLIDE_MOE_OK;
+  }
+  if (vec && y_dtype == FLIDE_BF16) {
+    combine_norm_bf16_kernel<u16, 8><<<T, RW_THREADS, 0, st>>>((const u16*)y, (const u16*)dense, sd,
+                                                               (const u16*)w1, (const u16*)w2, (u16*)out, so,
+                                                               H, k, eps);
+    FLIDE_CHECK_LAUNCH();
+    return FLIDE_MOE_OK;
+  }
   if (y_dtype == FLIDE_F32)
     combine_norm_kernel<FLIDE_F32><<<T, RW_THREADS, 0, st>>>(y, dense, sd, w1, w2, w_dtype, out, so,
                                                               out_dtype, H, k, eps);
