@@ -131,15 +131,18 @@ __global__ __launch_bounds__(256, OCC) void grouped_dma(GroupArgs p) {
   // c = (l % CPR) ^ swz(row). Instruction rows start at multiples of RPI, so swz(row) and therefore c
   // (and the chunk's K offset kc) depend on the lane only.
   const int kc = ((l % CPR) ^ swz<CPR>(l / CPR)) * (16 / EB);
-  const char* a_src[LA];
+  // Per-lane 32-bit byte offsets from the operands' uniform bases (A rows are gathered pairs, B rows
+  // the expert's weight rows); a stage adds its uniform K offset to the base, so a full stage's load is
+  // base (SGPRs) + offset (one VGPR). Both tensors stay below 4 GB.
+  uint32_t a_off32[LA];
 #pragma unroll
   for (int i = 0; i < LA; ++i) {
     const int row = (wave * LA + i) * RPI + l / CPR;
     const int pair = s_pairs[row];
     const long long src = pair < p.n_pairs ? (p.by_token ? pair / p.topk : pair) : 0;
-    a_src[i] = A + (src * p.sa + kc) * EB;
+    a_off32[i] = (uint32_t)((src * p.sa + kc) * EB);
   }
-  const char* b_src[LB];
+  uint32_t b_off32[LB];
 #pragma unroll
   for (int i = 0; i < LB; ++i) {
     const int row = (wave * LB + i) * RPI + l / CPR;
@@ -152,7 +155,7 @@ __global__ __launch_bounds__(256, OCC) void grouped_dma(GroupArgs p) {
       if (cc >= half) cc = half - 1;
       n = row < BN / 2 ? cc : cc + half;
     }
-    b_src[i] = B + (n * p.sbn + kc) * EB;
+    b_off32[i] = (uint32_t)((n * p.sbn + kc) * EB);
   }
 
   const int wm = wave % WAVES_M, wn = wave / WAVES_M;
@@ -203,21 +206,30 @@ __global__ __launch_bounds__(256, OCC) void grouped_dma(GroupArgs p) {
                    char* __restrict__ s3) {
     constexpr int FMA = decltype(fma_tag)::value;
     auto slot_ptr = [&](int slot) -> char* { return slot == 0 ? s0 : slot == 1 ? s1 : slot == 2 ? s2 : s3; };
-    // loads of stage kt into ring slot `slot`; K-tail chunks read zeros through a select, not a branch
+    // loads of a full stage kt (k0 + KS <= K) into ring slot `slot`: uniform base + lane offset
     auto issue = [&](int kt, int slot) {
+      FLIDE_LDS_AS char* sb = (FLIDE_LDS_AS char*)slot_ptr(slot);
+      const long long kb = (long long)kt * KS * EB;
+      const char* Ak = A + kb;
+      const char* Bk = B + kb;
+#pragma unroll
+      for (int i = 0; i < LA; ++i) dma16(Ak + a_off32[i], sb + (wave * LA + i) * 1024);
+#pragma unroll
+      for (int i = 0; i < LB; ++i) dma16(Bk + b_off32[i], sb + A_BYTES + (wave * LB + i) * 1024);
+    };
+    // the partial last stage (K % KS != 0): chunks past K read a 16-byte block of zeros
+    auto issue_tail = [&](int kt, int slot) {
       FLIDE_LDS_AS char* sb = (FLIDE_LDS_AS char*)slot_ptr(slot);
       const int k0 = kt * KS;
       const long long kb = (long long)k0 * EB;
+      const bool in = k0 + kc < K;
 #pragma unroll
-      for (int i = 0; i < LA; ++i) {
-        const void* src = (k0 + kc < K) ? (const void*)(a_src[i] + kb) : (const void*)g_zero16;
-        dma16(src, sb + (wave * LA + i) * 1024);
-      }
+      for (int i = 0; i < LA; ++i)
+        dma16(in ? (const void*)(A + kb + a_off32[i]) : (const void*)g_zero16, sb + (wave * LA + i) * 1024);
 #pragma unroll
-      for (int i = 0; i < LB; ++i) {
-        const void* src = (k0 + kc < K) ? (const void*)(b_src[i] + kb) : (const void*)g_zero16;
-        dma16(src, sb + A_BYTES + (wave * LB + i) * 1024);
-      }
+      for (int i = 0; i < LB; ++i)
+        dma16(in ? (const void*)(B + kb + b_off32[i]) : (const void*)g_zero16,
+              sb + A_BYTES + (wave * LB + i) * 1024);
     };
     auto compute = [&](int slot) {
       const char* sbase = slot_ptr(slot);
@@ -254,12 +266,13 @@ __global__ __launch_bounds__(256, OCC) void grouped_dma(GroupArgs p) {
         }
       }
     };
-    // prologue: the host guarantees nk >= NS - 1, so these loads are unconditional (a conditional load
-    // here would again make the wait-count pass conservative at the loop header)
+    // prologue: the host guarantees NS - 1 full stages, so these loads are unconditional (a conditional
+    // load here would again make the wait-count pass conservative at the loop header)
 #pragma unroll
     for (int st = 0; st < NS - 1; ++st) issue(st, st);
-    // steady state: stage kt computes while stages kt+1 .. kt+NS-1 load
-    const int nmain = nk - (NS - 1);   // iterations that issue a load
+    // steady state: stage kt computes while stages kt+1 .. kt+NS-1 load; every stage it issues is full
+    const int nfull = K / KS;
+    const int nmain = nfull - (NS - 1);   // iterations that issue a full stage
     int kt0 = 0;
     for (; kt0 + NS <= nmain; kt0 += NS) {
 #pragma unroll
@@ -270,14 +283,17 @@ __global__ __launch_bounds__(256, OCC) void grouped_dma(GroupArgs p) {
         compute(slot);
       }
     }
-    // drain: the remaining issuing iterations (fewer than NS) and the last NS - 1 stages
+    // drain: the remaining issuing iterations (fewer than NS, plus the partial stage if any) and the
+    // last NS - 1 stages
 #pragma unroll
-    for (int i = 0; i < 2 * NS - 2; ++i) {
+    for (int i = 0; i < 2 * NS - 1; ++i) {
       const int kt = kt0 + i;
       if (kt < nk) {
         wait_stage<NS, L>(min(NS - 2, nk - 1 - kt));
         __builtin_amdgcn_s_barrier();
-        if (kt + NS - 1 < nk) issue(kt + NS - 1, (i + NS - 1) % NS);
+        const int ks = kt + NS - 1;
+        if (ks < nfull) issue(ks, (i + NS - 1) % NS);
+        else if (ks < nk) issue_tail(ks, (i + NS - 1) % NS);
         compute(i % NS);
       }
     }
