@@ -200,8 +200,8 @@ __global__ __launch_bounds__(256, OCC) void grouped_dma(GroupArgs p) {
   // branch-free (unconditional loads, a constant wait count): control-flow joins make that pass fall
   // back to waiting for every outstanding load before each LDS read, collapsing the ring to one stage.
   const int nk = (K + KS - 1) / KS;
-  // FMA: fragment rows this block computes (all FM, or fewer when the waves span the whole block and
-  // its tail is padding: every wave then skips the same dead rows)
+  // FMA: fragment rows this wave computes: all FM, or fewer when its trailing fragments are padding
+  // (1 x 4 waves span the whole block and skip in steps of 4 fragments; 2 x 2 waves skip per fragment)
   auto kloop = [&](auto fma_tag, char* __restrict__ s0, char* __restrict__ s1, char* __restrict__ s2,
                    char* __restrict__ s3) {
     constexpr int FMA = decltype(fma_tag)::value;
@@ -233,7 +233,9 @@ __global__ __launch_bounds__(256, OCC) void grouped_dma(GroupArgs p) {
     };
     auto compute = [&](int slot) {
       const char* sbase = slot_ptr(slot);
-      if constexpr (FP8) {
+      if constexpr (FMA == 0) {
+        (void)sbase;   // every row of this wave is padding: loads and barriers only
+      } else if constexpr (FP8) {
         i32x8_t af[FMA], bfr[FN];
 #pragma unroll
         for (int fm = 0; fm < FMA; ++fm) {
@@ -306,6 +308,17 @@ __global__ __launch_bounds__(256, OCC) void grouped_dma(GroupArgs p) {
     else if (nlive <= 8) kloop(std::integral_constant<int, 8>{}, lds0, lds1, lds2, lds3);
     else if (nlive <= 12) kloop(std::integral_constant<int, 12>{}, lds0, lds1, lds2, lds3);
     else kloop(std::integral_constant<int, 16>{}, lds0, lds1, lds2, lds3);
+  } else if constexpr (WAVES_M > 1 && FM == 4) {
+    // each wave skips its trailing padding fragments (waves of the lower half of a partly filled
+    // block, or all of them, see padding only); the loads and barriers are the same in every variant
+    int nlive = 0;
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm) nlive += m_live[fm] ? 1 : 0;
+    if (nlive == 0) kloop(std::integral_constant<int, 0>{}, lds0, lds1, lds2, lds3);
+    else if (nlive == 1) kloop(std::integral_constant<int, 1>{}, lds0, lds1, lds2, lds3);
+    else if (nlive == 2) kloop(std::integral_constant<int, 2>{}, lds0, lds1, lds2, lds3);
+    else if (nlive == 3) kloop(std::integral_constant<int, 3>{}, lds0, lds1, lds2, lds3);
+    else kloop(std::integral_constant<int, 4>{}, lds0, lds1, lds2, lds3);
   } else {
     kloop(std::integral_constant<int, FM>{}, lds0, lds1, lds2, lds3);
   }
