@@ -33,10 +33,10 @@ using namespace grouped_detail;
 
 __device__ __attribute__((aligned(16))) const uint32_t g_zero16[4] = {0, 0, 0, 0};
 
-template <int N, int LGKM = 15> FLIDE_DEV void wait_vmcnt() {
+template <int N> FLIDE_DEV void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-  // s_waitcnt: vmcnt[3:0] bits 3:0, vmcnt[5:4] bits 15:14, expcnt (6:4) left open, lgkmcnt bits 11:8
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (LGKM << 8));
+  // s_waitcnt: vmcnt[3:0] bits 3:0, vmcnt[5:4] bits 15:14; expcnt (6:4) and lgkmcnt (11:8) left open
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
 FLIDE_DEV void dma16(const void* src, FLIDE_LDS_AS void* dst) {
@@ -47,20 +47,17 @@ FLIDE_DEV void dma16(const void* src, FLIDE_LDS_AS void* dst) {
 // measured bank-conflict-free for the fragment reads below
 template <int CPR> FLIDE_DEV int swz(int row) { return CPR == 8 ? (row & 7) : ((row >> 1) & 3); }
 
-// Waits until at most `ahead` (0 .. R-2) stages of this wave's loads are still in flight, each stage
-// L loads; LGKM = 0 also waits for this wave's outstanding LDS reads.
-template <int R, int L, int LGKM = 15> FLIDE_DEV void wait_stage(int ahead) {
-  static_assert(R >= 2 && R <= 5, "2..5 stages");
-  if constexpr (R >= 5) {
-    if (ahead >= 3) { wait_vmcnt<3 * L, LGKM>(); return; }
+// Waits until at most `ahead` (0 .. NS-2) stages of this wave's loads are still in flight (each stage =
+// L loads).
+template <int NS, int L> FLIDE_DEV void wait_stage(int ahead) {
+  static_assert(NS >= 2 && NS <= 4, "stage ring of 2..4");
+  if constexpr (NS >= 4) {
+    if (ahead >= 2) { wait_vmcnt<2 * L>(); return; }
   }
-  if constexpr (R >= 4) {
-    if (ahead >= 2) { wait_vmcnt<2 * L, LGKM>(); return; }
+  if constexpr (NS >= 3) {
+    if (ahead >= 1) { wait_vmcnt<L>(); return; }
   }
-  if constexpr (R >= 3) {
-    if (ahead >= 1) { wait_vmcnt<L, LGKM>(); return; }
-  }
-  wait_vmcnt<0, LGKM>();
+  wait_vmcnt<0>();
 }
 
 // Element type traits of the two kernel families: 16-bit (2 bytes, 64 K per 128-byte stage row, two
@@ -74,7 +71,7 @@ template <> struct DmaElem<Fp8Tag> {
 };
 
 template <typename T, typename OutT, int ACT, int BM, int BN, int WAVES_M, int WAVES_N, int NS, int ROWB, int OCC,
-          int XCD_CHUNK_BLOCKS, int LOOK>
+          int XCD_CHUNK_BLOCKS>
 __global__ __launch_bounds__(256, OCC) void grouped_dma(GroupArgs p) {
   constexpr bool FP8 = std::is_same<T, Fp8Tag>::value;
   constexpr int EB = DmaElem<T>::BYTES;
@@ -92,7 +89,7 @@ __global__ __launch_bounds__(256, OCC) void grouped_dma(GroupArgs p) {
   static_assert(WAVES_M * WAVES_N == 4, "4 waves");
   static_assert(BM % 32 == 0 && BN % 32 == 0, "tile rows come in 32s");
   static_assert(ACT == ACT_NONE || FN % 2 == 0, "gated tiles pair gate and up fragments");
-  static_assert((LOOK ? NS : NS - 1) * L < 64, "loads in flight must fit vmcnt");
+  static_assert((NS - 1) * L < 64, "loads in flight must fit vmcnt");
 
   // one LDS object per ring slot: distinct objects let the compiler see that reading slot s does not
   // alias the loads still landing in the other slots (it would otherwise wait for all of them)
@@ -273,117 +270,6 @@ __global__ __launch_bounds__(256, OCC) void grouped_dma(GroupArgs p) {
       }
     };
     const int nfull = K / KS;
-    if constexpr (LOOK) {
-      // Read-ahead ring (for one workgroup per CU, where no second workgroup hides the LDS latency):
-      // stage kt's MFMAs run on operands read one iteration earlier, and stage kt+1's reads are woven
-      // into them. Iteration kt: wait for this wave's loads of stage kt+1 and for its LDS reads of stage
-      // kt, barrier (stage kt+1 is in LDS for all, and nobody still reads slot kt % NS), refill slot
-      // kt % NS with stage kt+NS, then MFMAs of stage kt with the reads of stage kt+1. The operand
-      // with fewer fragments is read up front; the other runs as the outer MFMA loop and each of its
-      // fragments is re-read right after its last MFMA, into the registers it frees.
-      typedef typename std::conditional<FP8, i32x8_t, u32x4_t>::type Frag;
-      constexpr int FMR = FMA > 0 ? FMA : 1;
-      Frag fa[2][STEPS][FMR], fb[2][STEPS][FN];
-      auto ld = [&](const char* q) -> Frag {
-        if constexpr (FP8) {
-          const u32x4_t lo = *(const u32x4_t*)q;
-          const u32x4_t hi = *(const u32x4_t*)(q + (lane_off[1] - lane_off[0]));
-          return i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
-        } else {
-          return *(const u32x4_t*)q;
-        }
-      };
-      auto mma = [&](const Frag& a, const Frag& b, f32x4_t& c) {
-        if constexpr (FP8) c = mfma_fp8(a, b, c);
-        else c = Mfma16<T>::mma(a, b, c);
-      };
-      auto step = [&](int cur, int nxt, bool rd, int rslot) {
-        if constexpr (FMA > 0) {
-          const char* rb = slot_ptr(rslot);
-          if constexpr (FMA >= FN) {
-            if (rd) {
-#pragma unroll
-              for (int st = 0; st < STEPS; ++st)
-#pragma unroll
-                for (int fn = 0; fn < FN; ++fn) fb[nxt][st][fn] = ld(rb + b_off(fn, FP8 ? 0 : st));
-            }
-#pragma unroll
-            for (int fm = 0; fm < FMA; ++fm) {
-#pragma unroll
-              for (int st = 0; st < STEPS; ++st)
-#pragma unroll
-                for (int fn = 0; fn < FN; ++fn) mma(fa[cur][st][fm], fb[cur][st][fn], acc[fm][fn]);
-              if (rd) {
-#pragma unroll
-                for (int st = 0; st < STEPS; ++st) fa[nxt][st][fm] = ld(rb + a_off(fm, FP8 ? 0 : st));
-              }
-            }
-          } else {
-            if (rd) {
-#pragma unroll
-              for (int st = 0; st < STEPS; ++st)
-#pragma unroll
-                for (int fm = 0; fm < FMA; ++fm) fa[nxt][st][fm] = ld(rb + a_off(fm, FP8 ? 0 : st));
-            }
-#pragma unroll
-            for (int fn = 0; fn < FN; ++fn) {
-#pragma unroll
-              for (int st = 0; st < STEPS; ++st)
-#pragma unroll
-                for (int fm = 0; fm < FMA; ++fm) mma(fa[cur][st][fm], fb[cur][st][fn], acc[fm][fn]);
-              if (rd) {
-#pragma unroll
-                for (int st = 0; st < STEPS; ++st) fb[nxt][st][fn] = ld(rb + b_off(fn, FP8 ? 0 : st));
-              }
-            }
-          }
-        }
-      };
-      // prologue: the host guarantees NS full stages
-#pragma unroll
-      for (int st = 0; st < NS; ++st) issue(st, st);
-      wait_stage<NS + 1, L>(NS - 1);
-      __builtin_amdgcn_s_barrier();
-      if constexpr (FMA > 0) {
-        const char* rb = slot_ptr(0);
-#pragma unroll
-        for (int st = 0; st < STEPS; ++st) {
-#pragma unroll
-          for (int fm = 0; fm < FMA; ++fm) fa[0][st][fm] = ld(rb + a_off(fm, FP8 ? 0 : st));
-#pragma unroll
-          for (int fn = 0; fn < FN; ++fn) fb[0][st][fn] = ld(rb + b_off(fn, FP8 ? 0 : st));
-        }
-      }
-      // steady state, unrolled over NS slots x 2 register sets so both are compile-time constants
-      constexpr int UN = NS % 2 ? 2 * NS : NS;
-      const int nsteady = nfull - NS;   // iterations that issue a full stage
-      int kt0 = 0;
-      for (; kt0 + UN <= nsteady; kt0 += UN) {
-#pragma unroll
-        for (int i = 0; i < UN; ++i) {
-          wait_stage<NS + 1, L, 0>(NS - 2);
-          __builtin_amdgcn_s_barrier();
-          issue(kt0 + i + NS, i % NS);
-          step(i & 1, (i + 1) & 1, true, (i + 1) % NS);
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < UN + NS + 1; ++i) {
-        const int kt = kt0 + i;
-        if (kt < nk) {
-          const bool more = kt + 1 < nk;
-          if (more) {
-            wait_stage<NS + 1, L, 0>(min(NS - 2, nk - 2 - kt));
-            __builtin_amdgcn_s_barrier();
-            const int ks = kt + NS;
-            if (ks < nfull) issue(ks, i % NS);
-            else if (ks < nk) issue_tail(ks, i % NS);
-          }
-          step(i & 1, (i + 1) & 1, more, (i + 1) % NS);
-        }
-      }
-      return;
-    }
     // prologue: the host guarantees NS - 1 full stages, so these loads are unconditional (a conditional
     // load here would again make the wait-count pass conservative at the loop header)
 #pragma unroll
@@ -485,17 +371,17 @@ __global__ __launch_bounds__(256, OCC) void grouped_dma(GroupArgs p) {
 constexpr int DMA_BN = 256;
 
 template <typename T, typename OutT, int ACT, int BM, int WM_, int WN_, int NS, int ROWB, int OCC, int XB,
-          int LOOK = 0, int BN = DMA_BN>
+          int BN = DMA_BN>
 int launch_one(GroupArgs& p, hipStream_t st) {
   constexpr int KS = ROWB / DmaElem<T>::BYTES;
-  if (p.K < (LOOK ? NS : NS - 1) * KS) return FLIDE_MOE_ERR_TILE;   // the prologue's full stages
+  if (p.K < (NS - 1) * KS) return FLIDE_MOE_ERR_TILE;   // the ring needs NS - 1 full stages
   const int cols = ACT == ACT_NONE ? p.N : p.N / 2;
   const int per = ACT == ACT_NONE ? BN : BN / 2;
   p.ntn = (cols + per - 1) / per;
   const int items = p.nbm * p.ntn;
   const int round = 8 * p.ntn * XB;
   dim3 grid((items + round - 1) / round * round), block(256);
-  grouped_dma<T, OutT, ACT, BM, BN, WM_, WN_, NS, ROWB, OCC, XB, LOOK><<<grid, block, 0, st>>>(p);
+  grouped_dma<T, OutT, ACT, BM, BN, WM_, WN_, NS, ROWB, OCC, XB><<<grid, block, 0, st>>>(p);
   return FLIDE_MOE_OK;
 }
 
@@ -504,8 +390,8 @@ int launch_dma(GroupArgs& p, int bm, hipStream_t st) {
   constexpr bool FP8 = std::is_same<T, Fp8Tag>::value;
   if constexpr (FP8) {
     if (bm == 256) return launch_one<T, OutT, ACT, 256, 1, 4, 2, 128, 1, 2>(p, st);
-    if (bm == 128) return launch_one<T, OutT, ACT, 128, 2, 2, 2, 128, 2, 4, 0, 128>(p, st);
-    if (bm == 64) return launch_one<T, OutT, ACT, 64, 1, 4, 2, 128, 2, 8, 0, 128>(p, st);
+    if (bm == 128) return launch_one<T, OutT, ACT, 128, 2, 2, 2, 128, 2, 4, 128>(p, st);
+    if (bm == 64) return launch_one<T, OutT, ACT, 64, 1, 4, 2, 128, 2, 8, 128>(p, st);
   } else {
     if (bm == 256) return launch_one<T, OutT, ACT, 256, 1, 4, 4, 64, 1, 2>(p, st);
     if (bm == 128) return launch_one<T, OutT, ACT, 128, 2, 2, 3, 64, 2, 4>(p, st);
