@@ -159,7 +159,11 @@ def main() -> int:
         peak = MFMA_PEAK["fp8" if fp8 else "bf16"]
         roof = {"bound": "mfma", "achieved": gu_flops / k_s / 1e12, "peak": peak / 1e12, "unit": "TFLOP/s"}
     roof["frac"] = roof["achieved"] / roof["peak"]
-    roof["traffic"] = None
+    # HBM bytes per dispatch of this kernel at this workload, from the committed rocprofv3 --pmc summary
+    # (FETCH_SIZE + WRITE_SIZE scaled by a copy kernel of known size); None when not profiled
+    from flide_amd.rocprof import traffic_for
+    roof["traffic"] = traffic_for(cfg.name)
+    roof["algorithmic_bytes"] = gu_bytes
     roof["kernel"] = "grouped gate/up + GeGLU (" + ("fp8" if fp8 else "bf16") + f", bm {bm})"
     roof["kernel_us"] = k_s * 1e6
 
