@@ -601,7 +601,9 @@ __global__ __launch_bounds__(256) void grouped_stream8(GroupArgs p) {
 // ---------------------------------------------------------------------------------------------------
 // dispatch
 // ---------------------------------------------------------------------------------------------------
-// Compiled tiles: bm 16/32 -> stream kernels (4 waves x NF fragments); bm 64/128 -> LDS kernels.
+// Compiled tiles: bm 32/64/128/256 -> direct-to-LDS kernels (grouped_dma.hip); bm 16, and bm 32 when K is
+// too short for their ring -> stream kernels (4 waves x NF fragments); the register-staged LDS kernels
+// for bm 64/128 only under FLIDE_MOE_LEGACY_LDS=1 or for short K.
 #ifndef FLIDE_STREAM_NF
 #define FLIDE_STREAM_NF 2
 #endif
@@ -628,6 +630,12 @@ constexpr int STREAM_U = FLIDE_STREAM_U;   // K chunks in flight per wave
 template <typename T, typename OutT, int ACT>
 int launch16(GroupArgs& p, int bm, hipStream_t st) {
   dim3 block(256);
+  if (bm == 32 && !legacy_lds()) {   // the direct-to-LDS kernel streams whole lines (grouped_dma.hip)
+    const int out_dtype = std::is_same<OutT, float>::value ? FLIDE_F32
+                          : std::is_same<OutT, Bf16Out>::value ? FLIDE_BF16 : FLIDE_F16;
+    const int rc = dma_dispatch16(p, std::is_same<T, __bf16>::value, out_dtype, ACT, bm, st);
+    if (rc != FLIDE_MOE_ERR_TILE) return rc;   // else K is too short for the ring: the stream kernel
+  }
   if (bm == 16 || bm == 32) {
     constexpr int NF = ACT == ACT_NONE ? STREAM_NF_DOWN : STREAM_NF;
     constexpr int BNW = 4 * NF * 16;
@@ -661,6 +669,12 @@ int launch16(GroupArgs& p, int bm, hipStream_t st) {
 template <typename OutT, int ACT>
 int launch8(GroupArgs& p, int bm, hipStream_t st) {
   dim3 block(256);
+  if (bm == 32 && !legacy_lds()) {
+    const int out_dtype = std::is_same<OutT, float>::value ? FLIDE_F32
+                          : std::is_same<OutT, Bf16Out>::value ? FLIDE_BF16 : FLIDE_F16;
+    const int rc = dma_dispatch8(p, out_dtype, ACT, bm, st);
+    if (rc != FLIDE_MOE_ERR_TILE) return rc;   // else K is too short for the ring: the stream kernel
+  }
   if (bm == 16 || bm == 32) {
     constexpr int NF = ACT == ACT_NONE ? STREAM_NF_DOWN : STREAM_NF;
     constexpr int BNW = 4 * NF * 16;

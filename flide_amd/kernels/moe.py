@@ -32,12 +32,11 @@ BK8 = 128
 
 def tile(pairs: int, fp8: bool, device=None) -> tuple[int, int, int, int, int]:
     """(block rows, block columns, waves, stages, row blocks per group) for a layer of `pairs` pairs.
-    Block rows are what `align` pads each expert to: 16 or 32 rows run the streaming (decode) kernels,
-    whose weights go from HBM straight into MFMA registers; 64, 128 or 256 rows the LDS-tiled kernels.
-    The K order is the same for every tile, so the bits do not change with the choice."""
-    if pairs <= 2048:
-        bm = 16
-    elif pairs <= 8192:
+    Block rows are what `align` pads each expert to. 32 rows (decode) stream each expert's weights through
+    LDS in whole 128-byte lines; 16 rows stream them straight into MFMA registers (kept for callers that
+    ask for it); 64 and 128 rows are the prefill tiles. The K order is the same for every tile, so the
+    bits do not change with the choice."""
+    if pairs <= 4096:
         bm = 32
     elif pairs <= 16384:
         bm = 64

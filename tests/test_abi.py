@@ -139,8 +139,9 @@ def test_cpu_tensors_are_refused():
 def test_tile_choices():
     from flide_amd.kernels import moe
 
-    assert moe.tile(512, False)[0] == 16           # decode: streaming kernels
+    assert moe.tile(512, False)[0] == 32           # decode: weights streamed through LDS in whole lines
     assert moe.tile(4096, False)[0] == 32
+    assert moe.tile(8192, False)[0] == 64
     assert moe.tile(16384, False)[0] == 64
     assert moe.tile(65536, False)[0] == 128        # prefill: LDS-tiled kernels
     assert len(moe.tile(65536, True)) == 5

@@ -170,7 +170,7 @@ def test_experts_cfg1_decode():
 
 
 def test_experts_cfg1_shape_other_tiles():
-    """T = 512 .. 8192 at the Gemma shape run the bm 32 / 64 / 128 / 256 kernels."""
+    """T = 512 .. 8192 at the Gemma shape run the bm 32 / 64 / 128 kernels (bm 16 and 256: test_grouped_bf16)."""
     for T in (512, 2048, 4096, 8192):
         print(f"experts cfg1 T={T}", flush=True)
         sub = np.random.default_rng(T).choice(T * 8, 256, replace=False)
