@@ -139,6 +139,32 @@ def test_grouped_bf16(bm, by_token, mul_w, out32):
     assert_close(np32(out), ref, REL_BF16 if not out32 else 1e-5, "grouped")
 
 
+@pytest.mark.parametrize("bm", [16, 32, 64, 128, 256])
+@pytest.mark.parametrize("act", ["geglu", "swiglu"])
+def test_grouped_gated_tails(bm, act):
+    """The fused gate/up epilogue on every tile with tails in both directions: half = 100 output columns
+    (not a multiple of any tile's column count) and K = 200 (not a multiple of any stage width)."""
+    print(f"grouped gated bm={bm} {act}", flush=True)
+    from flide_amd import _hip
+
+    moe = _moe()
+    g = torch.Generator().manual_seed(100 + bm)
+    T, E, k, half, K = 80, 6, 2, 100, 200
+    _, ids = orc.route(torch.randn(T, E, generator=g).numpy(), k)
+    x = torch.randn(T, K, generator=g).to(torch.bfloat16)
+    w = (torch.randn(E, 2 * half, K, generator=g) * 0.08).to(torch.bfloat16)
+    rows, blocks, used = moe.align(torch.from_numpy(ids).to(DEV), E, bm)
+    out = torch.full((T * k, half), float("nan"), device=DEV, dtype=torch.bfloat16)
+    code = _hip.ACT_GEGLU if act == "geglu" else _hip.ACT_SWIGLU
+    moe.grouped(x.to(DEV), w.to(DEV), out, rows, blocks, used, k, True, tile=(bm, 128, 4, 2), act=code)
+    al = orc.align(ids, E, bm)
+    gu = orc.grouped(np32(x), np32(w), al["rows"], al["blocks"], al["used"], T * k, k, True, bm=bm,
+                     out_dtype="bf16")
+    ref = orc.geglu(gu[:, :half], gu[:, half:]) if act == "geglu" else orc.swiglu(gu, half)
+    assert not np.isnan(np32(out)).any(), "a valid pair's row was not written"
+    assert_close(np32(out), ref, REL_BF16, f"gated bm={bm} {act}")
+
+
 def _experts_case(cfg, T=None, pairs_subset=None, fp8=False):
     moe = _moe()
     d = inputs(cfg, 0, T)
