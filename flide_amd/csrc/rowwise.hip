@@ -219,6 +219,55 @@ __global__ __launch_bounds__(RW_THREADS) void quantize_rows_kernel(const void* _
   }
 }
 
+// 16-bit rows, K % 8 == 0, K <= NV * 512: one wave per row (4 rows per workgroup). The row is loaded
+// once in 16-byte pieces and kept in registers between the amax and the quantization; each lane stores
+// 8 quantized bytes at a time. Same arithmetic as quantize_rows_kernel (a true float32 division).
+template <int NV, bool BF16>
+__global__ __launch_bounds__(RW_THREADS) void quantize_rows_vec_kernel(const u16* __restrict__ x, long long sx,
+                                                                       int K, int M, u8* __restrict__ q,
+                                                                       long long sq, float* __restrict__ s) {
+  const int l = threadIdx.x & 63;
+  const long long row = (long long)blockIdx.x * (RW_THREADS / 64) + (threadIdx.x >> 6);
+  if (row >= M) return;
+  const int nv = K / 8;
+  const uint4* xr = (const uint4*)(x + row * sx);
+  uint4 raw[NV];
+  float amax = 0.f;
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int c = l + v * 64;
+    raw[v] = c < nv ? xr[c] : make_uint4(0, 0, 0, 0);
+  }
+  auto val = [](uint32_t w, int hi) {
+    const u16 h = hi ? (u16)(w >> 16) : (u16)(w & 0xffff);
+    return BF16 ? bf16_to_f32(h) : f16_to_f32(h);
+  };
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const uint32_t w[4] = {raw[v].x, raw[v].y, raw[v].z, raw[v].w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(val(w[i >> 1], i & 1)));
+  }
+  amax = wave_max(amax);
+  const float sc = fmaxf(amax, 1e-12f) * (1.0f / 448.0f);
+  if (l == 0) s[row] = sc;
+  uint2* qr = (uint2*)(q + row * sq);
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int c = l + v * 64;
+    if (c >= nv) continue;
+    const uint32_t w[4] = {raw[v].x, raw[v].y, raw[v].z, raw[v].w};
+    uint32_t packed[2] = {0, 0};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float t = val(w[i >> 1], i & 1) / sc;   // correctly rounded division
+      t = fminf(fmaxf(t, -448.0f), 448.0f);
+      packed[i >> 2] |= (uint32_t)f32_to_e4m3fn(t) << (8 * (i & 3));
+    }
+    qr[c] = make_uint2(packed[0], packed[1]);
+  }
+}
+
 // ---------------------------------------------------------------------------------------------------
 // RMSNorm without residual
 // ---------------------------------------------------------------------------------------------------
@@ -323,7 +372,29 @@ extern "C" int flide_moe_quantize_rows(const void* x, long long sx, int M, int K
                                        void* q, long long sq, float* s, flide_stream_t stream) {
   if (M < 0 || K < 0 || !dtype_ok(x_dtype)) return FLIDE_MOE_ERR_ARG;
   if (M == 0) return FLIDE_MOE_OK;
-  quantize_rows_kernel<<<M, RW_THREADS, 0, (hipStream_t)stream>>>(x, sx, K, x_dtype, (u8*)q, sq, s);
+  hipStream_t st = (hipStream_t)stream;
+  const bool vec = x_dtype != FLIDE_F32 && K % 8 == 0 && K <= 16 * 512 && sx % 8 == 0 && sq % 8 == 0 &&
+                   !((uintptr_t)x & 15) && !((uintptr_t)q & 7);
+  if (vec) {
+    const int per_lane = (K / 8 + 63) / 64;
+    const dim3 grid((M + 3) / 4);
+#define QV(NV)                                                                                            \
+  do {                                                                                                     \
+    if (x_dtype == FLIDE_BF16)                                                                             \
+      quantize_rows_vec_kernel<NV, true><<<grid, RW_THREADS, 0, st>>>((const u16*)x, sx, K, M, (u8*)q, sq, s); \
+    else                                                                                                   \
+      quantize_rows_vec_kernel<NV, false><<<grid, RW_THREADS, 0, st>>>((const u16*)x, sx, K, M, (u8*)q, sq, s); \
+  } while (0)
+    if (per_lane <= 1) QV(1);
+    else if (per_lane <= 2) QV(2);
+    else if (per_lane <= 4) QV(4);
+    else if (per_lane <= 8) QV(8);
+    else QV(16);
+#undef QV
+    FLIDE_CHECK_LAUNCH();
+    return FLIDE_MOE_OK;
+  }
+  quantize_rows_kernel<<<M, RW_THREADS, 0, st>>>(x, sx, K, x_dtype, (u8*)q, sq, s);
   FLIDE_CHECK_LAUNCH();
   return FLIDE_MOE_OK;
 }

@@ -249,13 +249,17 @@ def test_combine_qwen():
     np.testing.assert_allclose(np32(out), ref, rtol=2 ** -7, atol=1e-6)
 
 
-@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
-def test_quantize_rows_bit_exact(dt):
-    print(f"quantize {dt}", flush=True)
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32, torch.float16])
+@pytest.mark.parametrize("K", [704, 2816, 136])
+def test_quantize_rows_bit_exact(dt, K):
+    """Scales and e4m3 bytes bit-exact: 16-bit rows take the one-wave-per-row vector kernel (K = 136 and
+    704 and 2816 use 1, 2 and 8 register pieces per lane), float32 rows the per-element kernel."""
+    print(f"quantize {dt} K={K}", flush=True)
     from flide_amd.kernels import fp8
 
     g = torch.Generator().manual_seed(13)
-    x = torch.randn(97, 704, generator=g) * torch.logspace(-6, 3, 97).unsqueeze(1)
+    scale = torch.logspace(-6, 3, 97) if dt != torch.float16 else torch.logspace(-3, 3, 97)
+    x = torch.randn(97, K, generator=g) * scale.unsqueeze(1)
     x[3] = 0.0
     x[5, :10] = torch.tensor([448.0, -448.0, 1e-30, -1e-30, 0.0, -0.0, 3.0, 5e-3, 1e-8, 2.0])
     x = x.to(dt)
