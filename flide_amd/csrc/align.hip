@@ -49,13 +49,15 @@ __global__ __launch_bounds__(ALIGN_THREADS) void align_place(const int* __restri
   __shared__ int before[ALIGN_MAX_E];  // this expert's pairs in earlier chunks
   __shared__ int cnt[ALIGN_MAX_E];     // total pairs per expert
   __shared__ int wcur[ALIGN_WAVES][ALIGN_MAX_E];
-  __shared__ int scan_tmp[ALIGN_THREADS];
+  __shared__ int scan_tmp[ALIGN_WAVES];
   const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63;
   const int c = blockIdx.x;
 
   const int cbase = c * ALIGN_CHUNK;
-  const int wbase = cbase + wave * ALIGN_PER_WAVE;
-  const int wend = min(n, wbase + ALIGN_PER_WAVE);
+  // this wave's pairs: a quarter of the chunk (FUSED: of all n pairs, in 64-pair steps), in pair order
+  const int wper = FUSED ? (n + 4 * 64 - 1) / (4 * 64) * 64 : ALIGN_PER_WAVE;
+  const int wbase = cbase + wave * wper;
+  const int wend = min(n, wbase + wper);
   if constexpr (FUSED) {
     // one chunk holds every pair: count them here (per wave, which the placement needs anyway)
     for (int e = l; e < E; e += 64) wcur[wave][e] = 0;
@@ -85,22 +87,24 @@ __global__ __launch_bounds__(ALIGN_THREADS) void align_place(const int* __restri
     }
   }
   __syncthreads();
-  // exclusive scan of the padded counts over experts: each thread owns a run of ceil(E / 256)
+  // exclusive scan of the padded counts over experts: each thread owns a run of ceil(E / 256); a
+  // shuffle scan inside each wave, then the waves' totals
   const int per = (E + ALIGN_THREADS - 1) / ALIGN_THREADS;
   int run = 0;
   for (int j = 0; j < per; ++j) {
     int e = tid * per + j;
     if (e < E) run += (cnt[e] + bm - 1) / bm * bm;
   }
-  scan_tmp[tid] = run;
-  __syncthreads();
-  for (int o = 1; o < ALIGN_THREADS; o <<= 1) {
-    int v = tid >= o ? scan_tmp[tid - o] : 0;
-    __syncthreads();
-    scan_tmp[tid] += v;
-    __syncthreads();
+  int incl = run;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int v = __shfl_up(incl, o);
+    if (l >= o) incl += v;
   }
-  int acc = scan_tmp[tid] - run;
+  if (l == 63) scan_tmp[wave] = incl;
+  __syncthreads();
+  int acc = incl - run;
+  for (int w = 0; w < wave; ++w) acc += scan_tmp[w];
   for (int j = 0; j < per; ++j) {
     int e = tid * per + j;
     if (e < E) {
