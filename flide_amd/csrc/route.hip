@@ -113,7 +113,7 @@ __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ lo
     if (l + 64 * i < E) s += expf(v[i] - m);
   s = wave_sum(s);
   unsigned taken = 0;
-  float my_p = 0.f, topsum = 0.f;
+  float my_v = -INFINITY;   // lane j < k: the j-th selected logit and its id
   int my_id = 0;
   for (int j = 0; j < k; ++j) {
     float bv = -INFINITY;
@@ -130,13 +130,15 @@ __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ lo
     }
     wave_argmax(bv, bi);
     if (bi != INT_MAX && (bi & 63) == l) taken |= 1u << (bi >> 6);
-    float p = expf(bv - m) / s;
-    topsum += p;
     if (l == j) {
-      my_p = p;
+      my_v = bv;
       my_id = bi;
     }
   }
+  // probabilities of the selected experts, summed in slot order (lane reads of lanes 0..k-1)
+  const float my_p = l < k ? expf(my_v - m) / s : 0.f;
+  float topsum = 0.f;
+  for (int j = 0; j < k; ++j) topsum += __shfl(my_p, j);
   if (l < k) {
     float ww = my_p / topsum;
     if (scale) ww *= load_scalar(scale, scale_dtype, my_id);
