@@ -602,8 +602,8 @@ __global__ __launch_bounds__(256) void grouped_stream8(GroupArgs p) {
 // dispatch
 // ---------------------------------------------------------------------------------------------------
 // Compiled tiles: bm 32/64/128/256 -> direct-to-LDS kernels (grouped_dma.hip); bm 16, and bm 32 when K is
-// too short for their ring -> stream kernels (4 waves x NF fragments); the register-staged LDS kernels
-// for bm 64/128 only under FLIDE_MOE_LEGACY_LDS=1 or for short K.
+// too short for their ring -> stream kernels (4 waves x NF fragments); bm 64/128/256 with K too short
+// for the ring (or under FLIDE_MOE_LEGACY_LDS=1) -> the register-staged LDS kernels below.
 #ifndef FLIDE_STREAM_NF
 #define FLIDE_STREAM_NF 2
 #endif
@@ -653,14 +653,15 @@ int launch16(GroupArgs& p, int bm, hipStream_t st) {
     const int rc = dma_dispatch16(p, std::is_same<T, __bf16>::value, out_dtype, ACT, bm, st);
     if (rc != FLIDE_MOE_ERR_TILE) return rc;   // else K is too short for the ring: the LDS kernel below
   }
-  if (bm == 64 || bm == 128) {
+  if (bm == 64 || bm == 128 || bm == 256) {
     constexpr int BN = 128;
     const int cols = ACT == ACT_NONE ? p.N : p.N / 2;
     const int per = ACT == ACT_NONE ? BN : BN / 2;
     p.ntn = (cols + per - 1) / per;
     dim3 grid(p.nbm * p.ntn);
     if (bm == 64) grouped_lds16<T, OutT, ACT, 64, BN, 2, 2><<<grid, block, 0, st>>>(p);
-    else grouped_lds16<T, OutT, ACT, 128, BN, 2, 2><<<grid, block, 0, st>>>(p);
+    else if (bm == 128) grouped_lds16<T, OutT, ACT, 128, BN, 2, 2><<<grid, block, 0, st>>>(p);
+    else grouped_lds16<T, OutT, ACT, 256, BN, 2, 2><<<grid, block, 0, st>>>(p);
     return FLIDE_MOE_OK;
   }
   return FLIDE_MOE_ERR_TILE;
@@ -692,14 +693,15 @@ int launch8(GroupArgs& p, int bm, hipStream_t st) {
     const int rc = dma_dispatch8(p, out_dtype, ACT, bm, st);
     if (rc != FLIDE_MOE_ERR_TILE) return rc;   // else K is too short for the ring: the LDS kernel below
   }
-  if (bm == 64 || bm == 128) {
+  if (bm == 64 || bm == 128 || bm == 256) {
     constexpr int BN = 128;
     const int cols = ACT == ACT_NONE ? p.N : p.N / 2;
     const int per = ACT == ACT_NONE ? BN : BN / 2;
     p.ntn = (cols + per - 1) / per;
     dim3 grid(p.nbm * p.ntn);
     if (bm == 64) grouped_lds8<OutT, ACT, 64, BN, 2, 2><<<grid, block, 0, st>>>(p);
-    else grouped_lds8<OutT, ACT, 128, BN, 2, 2><<<grid, block, 0, st>>>(p);
+    else if (bm == 128) grouped_lds8<OutT, ACT, 128, BN, 2, 2><<<grid, block, 0, st>>>(p);
+    else grouped_lds8<OutT, ACT, 256, BN, 2, 2><<<grid, block, 0, st>>>(p);
     return FLIDE_MOE_OK;
   }
   return FLIDE_MOE_ERR_TILE;

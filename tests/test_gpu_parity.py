@@ -165,6 +165,35 @@ def test_grouped_gated_tails(bm, act):
     assert_close(np32(out), ref, REL_BF16, f"gated bm={bm} {act}")
 
 
+@pytest.mark.parametrize("bm", [16, 32, 64, 128, 256])
+@pytest.mark.parametrize("fp8,K", [(False, 8), (False, 40), (True, 16), (True, 48)])
+def test_grouped_short_k(bm, fp8, K):
+    """K shorter than every tile's stage ring: each tile has to fall back to a kernel without one."""
+    print(f"grouped short K bm={bm} fp8={fp8} K={K}", flush=True)
+    moe = _moe()
+    g = torch.Generator().manual_seed(7 * bm + K)
+    T, E, k, N = 72, 5, 2, 96
+    _, ids = orc.route(torch.randn(T, E, generator=g).numpy(), k)
+    x = torch.randn(T, K, generator=g).to(torch.bfloat16)
+    w = (torch.randn(E, N, K, generator=g) * 0.1).to(torch.bfloat16)
+    rows, blocks, used = moe.align(torch.from_numpy(ids).to(DEV), E, bm)
+    out = torch.full((T * k, N), float("nan"), device=DEV, dtype=torch.bfloat16)
+    al = orc.align(ids, E, bm)
+    if fp8:
+        qw, sw = orc.quantize_experts(np32(w))
+        qx, sx = orc.quantize_tokens(np32(x))
+        wq = torch.from_numpy(orc.e4m3fn_encode(qw)).view(torch.float8_e4m3fn).to(DEV)
+        moe.grouped_fp8(x.to(DEV), wq, torch.from_numpy(sw).to(DEV), out, rows, blocks, used, k, True,
+                        tile=(bm, 128, 4, 2))
+        a_ref, w_ref = qx * sx, qw * sw[:, :, None]   # the dequantised computation
+    else:
+        moe.grouped(x.to(DEV), w.to(DEV), out, rows, blocks, used, k, True, tile=(bm, 128, 4, 2))
+        a_ref, w_ref = np32(x), np32(w)
+    ref = orc.grouped(a_ref, w_ref, al["rows"], al["blocks"], al["used"], T * k, k, True, bm=bm, out_dtype="bf16")
+    assert not np.isnan(np32(out)).any(), "a valid pair's row was not written"
+    assert_close(np32(out), ref, REL_BF16, f"short K bm={bm}")
+
+
 def _experts_case(cfg, T=None, pairs_subset=None, fp8=False):
     moe = _moe()
     d = inputs(cfg, 0, T)
