@@ -75,9 +75,17 @@ def e4m3fn_decode(code) -> np.ndarray:
     return (s * v).astype(np.float32)
 
 
+def f16_round(x) -> np.ndarray:
+    """Round to IEEE binary16 (numpy's cast: round to nearest even, overflow to inf) and back to float32."""
+    with np.errstate(over="ignore"):   # overflow to inf is the defined result
+        return np.asarray(x, np.float32).astype(np.float16).astype(np.float32)
+
+
 def _round(x, dtype: str) -> np.ndarray:
     x = np.asarray(x, dtype=np.float32)
-    return bf16_round(x) if dtype == "bf16" else x
+    if dtype == "bf16":
+        return bf16_round(x)
+    return f16_round(x) if dtype == "f16" else x
 
 
 # ----------------------------------------------------------------------------------------------------

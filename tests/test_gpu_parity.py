@@ -118,30 +118,34 @@ def test_align_configs_exact(cfg):
 # --------------------------------------------------------------------------------------------------
 @pytest.mark.parametrize("bm", [16, 32, 64, 128, 256])
 @pytest.mark.parametrize("by_token,mul_w,out32", [(True, False, False), (False, True, True)])
-def test_grouped_bf16(bm, by_token, mul_w, out32):
-    print(f"grouped bm={bm} by_token={by_token}", flush=True)
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+def test_grouped_bf16(bm, by_token, mul_w, out32, dt):
+    """Plain grouped products (16-bit rows and experts, 16-bit or float32 out) on every tile."""
+    print(f"grouped bm={bm} by_token={by_token} {dt}", flush=True)
     moe = _moe()
     g = torch.Generator().manual_seed(bm)
     T, E, k, N, K = 96, 12, 3, 200, 136
     logits = torch.randn(T, E, generator=g)
     _, ids = orc.route(logits.numpy(), k)
     rows_in = T if by_token else T * k
-    a = torch.randn(rows_in, K, generator=g).to(torch.bfloat16)
-    w = (torch.randn(E, N, K, generator=g) * 0.05).to(torch.bfloat16)
+    a = torch.randn(rows_in, K, generator=g).to(dt)
+    w = (torch.randn(E, N, K, generator=g) * 0.05).to(dt)
     wts = torch.rand(T * k, generator=g)
     rows, blocks, used = moe.align(torch.from_numpy(ids).to(DEV), E, bm)
-    out = torch.full((T * k, N), float("nan"), device=DEV, dtype=torch.float32 if out32 else torch.bfloat16)
+    out = torch.full((T * k, N), float("nan"), device=DEV, dtype=torch.float32 if out32 else dt)
     moe.grouped(a.to(DEV), w.to(DEV), out, rows, blocks, used, k, by_token, wts.to(DEV) if mul_w else None,
                 tile=(bm, 128, 4, 2))
     al = orc.align(ids, E, bm)
+    odt = "fp32" if out32 else ("bf16" if dt == torch.bfloat16 else "f16")
     ref = orc.grouped(np32(a), np32(w), al["rows"], al["blocks"], al["used"], T * k, k, by_token,
-                      wts.numpy() if mul_w else None, bm=bm, out_dtype="fp32" if out32 else "bf16")
+                      wts.numpy() if mul_w else None, bm=bm, out_dtype=odt)
     assert_close(np32(out), ref, REL_BF16 if not out32 else 1e-5, "grouped")
 
 
 @pytest.mark.parametrize("bm", [16, 32, 64, 128, 256])
 @pytest.mark.parametrize("act", ["geglu", "swiglu"])
-def test_grouped_gated_tails(bm, act):
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+def test_grouped_gated_tails(bm, act, dt):
     """The fused gate/up epilogue on every tile with tails in both directions: half = 100 output columns
     (not a multiple of any tile's column count) and K = 200 (not a multiple of any stage width)."""
     print(f"grouped gated bm={bm} {act}", flush=True)
@@ -151,16 +155,16 @@ def test_grouped_gated_tails(bm, act):
     g = torch.Generator().manual_seed(100 + bm)
     T, E, k, half, K = 80, 6, 2, 100, 200
     _, ids = orc.route(torch.randn(T, E, generator=g).numpy(), k)
-    x = torch.randn(T, K, generator=g).to(torch.bfloat16)
-    w = (torch.randn(E, 2 * half, K, generator=g) * 0.08).to(torch.bfloat16)
+    x = torch.randn(T, K, generator=g).to(dt)
+    w = (torch.randn(E, 2 * half, K, generator=g) * 0.08).to(dt)
     rows, blocks, used = moe.align(torch.from_numpy(ids).to(DEV), E, bm)
-    out = torch.full((T * k, half), float("nan"), device=DEV, dtype=torch.bfloat16)
+    out = torch.full((T * k, half), float("nan"), device=DEV, dtype=dt)
     code = _hip.ACT_GEGLU if act == "geglu" else _hip.ACT_SWIGLU
     moe.grouped(x.to(DEV), w.to(DEV), out, rows, blocks, used, k, True, tile=(bm, 128, 4, 2), act=code)
     al = orc.align(ids, E, bm)
-    gu = orc.grouped(np32(x), np32(w), al["rows"], al["blocks"], al["used"], T * k, k, True, bm=bm,
-                     out_dtype="bf16")
-    ref = orc.geglu(gu[:, :half], gu[:, half:]) if act == "geglu" else orc.swiglu(gu, half)
+    odt = "bf16" if dt == torch.bfloat16 else "f16"
+    gu = orc.grouped(np32(x), np32(w), al["rows"], al["blocks"], al["used"], T * k, k, True, bm=bm, out_dtype=odt)
+    ref = orc.geglu(gu[:, :half], gu[:, half:], odt) if act == "geglu" else orc.swiglu(gu, half, odt)
     assert not np.isnan(np32(out)).any(), "a valid pair's row was not written"
     assert_close(np32(out), ref, REL_BF16, f"gated bm={bm} {act}")
 

@@ -39,6 +39,15 @@ def test_bf16_round_matches_torch():
     assert np.isnan(orc.bf16_round(np.array([np.nan], np.float32))).all()
 
 
+def test_f16_round_matches_torch():
+    g = torch.Generator().manual_seed(1)
+    x = torch.cat([torch.randn(200000, generator=g) * 30,
+                   torch.tensor([0.0, -0.0, 65504.0, 65520.0, -70000.0, 6e-8, 3e-8, -1e-9]),
+                   # exact ties between two half values: lsb even and odd
+                   torch.tensor([1.0 + 2 ** -11, 1.0 + 3 * 2 ** -11, -(1.0 + 2 ** -11)])])
+    np.testing.assert_array_equal(orc.f16_round(x.numpy()), x.half().float().numpy())
+
+
 def test_e4m3fn_round_matches_torch():
     g = torch.Generator().manual_seed(1)
     codes = torch.arange(256, dtype=torch.uint8)
