@@ -1,6 +1,6 @@
 // Prefill-shaped grouped products: direct-to-LDS loads, a multi-stage ring and large MFMA tiles.
 //
-// One workgroup (4 waves, one per SIMD) computes a BM-row block of pairs (one expert, as align padded
+// One workgroup (4 or 8 waves) computes a BM-row block of pairs (one expert, as align padded
 // it) against a BN-row tile of that expert's weight. Per K stage it moves (BM + BN) rows of 128 bytes
 // straight from global memory into LDS with global_load_lds_dwordx4 (gfx950): no VGPR staging, no LDS
 // write instructions. NS stages are in flight: while the MFMAs consume stage kt, the loads of stages
@@ -72,7 +72,7 @@ template <> struct DmaElem<Fp8Tag> {
 
 template <typename T, typename OutT, int ACT, int BM, int BN, int WAVES_M, int WAVES_N, int NS, int ROWB, int OCC,
           int XCD_CHUNK_BLOCKS>
-__global__ __launch_bounds__(256, OCC) void grouped_dma(GroupArgs p) {
+__global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void grouped_dma(GroupArgs p) {
   constexpr bool FP8 = std::is_same<T, Fp8Tag>::value;
   constexpr int EB = DmaElem<T>::BYTES;
   constexpr int KS = ROWB / EB;                // K values per stage
@@ -80,13 +80,14 @@ __global__ __launch_bounds__(256, OCC) void grouped_dma(GroupArgs p) {
   constexpr int RPI = 64 / CPR;                // rows one 1 KB load instruction fills
   constexpr int STEPS = FP8 ? 1 : ROWB / 64;   // MFMA K steps per stage
   constexpr int A_BYTES = BM * ROWB, B_BYTES = BN * ROWB, STAGE = A_BYTES + B_BYTES;
-  constexpr int LA = BM / (4 * RPI), LB = BN / (4 * RPI);   // 1 KB loads per wave per stage
+  constexpr int NW = WAVES_M * WAVES_N;                      // waves per workgroup
+  constexpr int LA = BM / (NW * RPI), LB = BN / (NW * RPI);  // 1 KB loads per wave per stage
   static_assert(!FP8 || ROWB == 128, "float8 stages hold one 128-wide MFMA step");
-  static_assert(BM % (4 * RPI) == 0 && BN % (4 * RPI) == 0, "tile rows split over 4 waves");
+  static_assert(BM % (NW * RPI) == 0 && BN % (NW * RPI) == 0, "tile rows split over the waves");
   constexpr int L = LA + LB;
   constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
   constexpr int FM = WM / 16, FN = WN / 16;
-  static_assert(WAVES_M * WAVES_N == 4, "4 waves");
+  static_assert(NW == 4 || NW == 8, "4 or 8 waves");
   static_assert(BM % 32 == 0 && BN % 32 == 0, "tile rows come in 32s");
   static_assert(ACT == ACT_NONE || FN % 2 == 0, "gated tiles pair gate and up fragments");
   static_assert((NS - 1) * L < 64, "loads in flight must fit vmcnt");
@@ -113,7 +114,7 @@ __global__ __launch_bounds__(256, OCC) void grouped_dma(GroupArgs p) {
   const int pm = widx / p.ntn, pn = widx % p.ntn;
   if (pm >= p.nbm || pm * BM >= *p.used) return;
   const long long e = p.blocks[pm];
-  for (int r = tid; r < BM; r += 256) {
+  for (int r = tid; r < BM; r += NW * 64) {
     const int pair = p.rows[pm * BM + r];
     s_pairs[r] = pair;
     if constexpr (FP8) {
@@ -364,7 +365,8 @@ __global__ __launch_bounds__(256, OCC) void grouped_dma(GroupArgs p) {
 // tiles here (measured: the one-workgroup variants lose 15-40% on gfx950), so the ring fits in 80 KB:
 //  bm 256 (16-bit): 1 x 4 waves of 256 x 64, 64-byte stage rows, 4 stages = 128 KB, one workgroup per CU;
 //     the waves share all 256 rows, so a block's padded tail costs no MFMA time
-//  bm 128 (16-bit): 2 x 2 waves of 64 x 128, 64-byte stage rows, 3 stages = 72 KB, two workgroups per CU
+//  bm 128 (16-bit): 2 x 2 waves of 64 x 128, 64-byte stage rows, 3 stages = 72 KB, two workgroups per CU;
+//     the plain (down) product: 2 x 4 waves of 64 x 64 in one 512-thread workgroup (645 -> 598 us)
 //  bm 64  (16-bit): 1 x 4 waves of 64 x 64, 64-byte stage rows, 3 stages = 60 KB, two workgroups per CU
 //  float8 (128-byte stage rows, one 128-wide MFMA step): bm 128 and 64 with BN = 128 and 2 stages
 //     (64 / 48 KB, two or three workgroups per CU), bm 128 plain (down) products with BN = 64 (48 KB,
@@ -386,7 +388,7 @@ int launch_one(GroupArgs& p, hipStream_t st) {
   p.ntn = (cols + per - 1) / per;
   const int items = p.nbm * p.ntn;
   const int round = 8 * p.ntn * XB;
-  dim3 grid((items + round - 1) / round * round), block(256);
+  dim3 grid((items + round - 1) / round * round), block(WM_ * WN_ * 64);
   grouped_dma<T, OutT, ACT, BM, BN, WM_, WN_, NS, ROWB, OCC, XB><<<grid, block, 0, st>>>(p);
   return FLIDE_MOE_OK;
 }
@@ -408,7 +410,10 @@ int launch_dma(GroupArgs& p, int bm, hipStream_t st) {
       else return launch_one<T, OutT, ACT, 32, 2, 2, 3, 128, 3, 4, 64>(p, st);
     }
     if (bm == 256) return launch_one<T, OutT, ACT, 256, 1, 4, 4, 64, 1, 2>(p, st);
-    if (bm == 128) return launch_one<T, OutT, ACT, 128, 2, 2, 3, 64, 2, 4>(p, st);
+    if (bm == 128) {   // plain (down) products: 8 waves of 64 x 64, two per SIMD within one workgroup
+      if constexpr (ACT == ACT_NONE) return launch_one<T, OutT, ACT, 128, 2, 4, 3, 64, 1, 4>(p, st);
+      else return launch_one<T, OutT, ACT, 128, 2, 2, 3, 64, 2, 4>(p, st);
+    }
     if (bm == 64) return launch_one<T, OutT, ACT, 64, 1, 4, 3, 64, 2, 8>(p, st);
   }
   return FLIDE_MOE_ERR_TILE;
