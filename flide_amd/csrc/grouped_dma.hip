@@ -369,8 +369,8 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void grouped_dma(Group
 //     the plain (down) product: 2 x 4 waves of 64 x 64 in one 512-thread workgroup (645 -> 598 us)
 //  bm 64  (16-bit): 1 x 4 waves of 64 x 64, 64-byte stage rows, 3 stages = 60 KB, two workgroups per CU
 //  float8 (128-byte stage rows, one 128-wide MFMA step): bm 128 and 64 with BN = 128 and 2 stages
-//     (64 / 48 KB, two or three workgroups per CU), bm 128 plain (down) products with BN = 64 (48 KB,
-//     three per CU: 375 -> 342 us at 4096 tokens); bm 256: 2 stages = 128 KB
+//     (64 / 48 KB, two or three workgroups per CU); the bm-128 plain (down) product in 8 waves of
+//     64 x 32 (375 -> 290 us at 4096 tokens); bm 256: 2 stages = 128 KB
 //  bm 32 (decode): 128-byte stage rows, 3 stages. 16-bit: BN = 64 (gated 2 x 2 waves, plain 1 x 4),
 //     36 KB, three workgroups per CU; float8: 1 x 4 waves, BN = 128, 60 KB. Weight-streaming bound:
 //     whole 128-byte lines per row and stage read measurably faster than the half-line pairs of the
@@ -399,8 +399,8 @@ int launch_dma(GroupArgs& p, int bm, hipStream_t st) {
   if constexpr (FP8) {
     if (bm == 32) return launch_one<T, OutT, ACT, 32, 1, 4, 3, 128, 2, 8, 128>(p, st);
     if (bm == 256) return launch_one<T, OutT, ACT, 256, 1, 4, 2, 128, 1, 2>(p, st);
-    if (bm == 128) {   // the down product (K = 704: few stages) gains from a third workgroup per CU
-      if constexpr (ACT == ACT_NONE) return launch_one<T, OutT, ACT, 128, 2, 2, 2, 128, 3, 4, 64>(p, st);
+    if (bm == 128) {   // the plain (down) product: 8 waves of 64 x 32
+      if constexpr (ACT == ACT_NONE) return launch_one<T, OutT, ACT, 128, 2, 4, 2, 128, 2, 4, 128>(p, st);
       else return launch_one<T, OutT, ACT, 128, 2, 2, 2, 128, 2, 4, 128>(p, st);
     }
     if (bm == 64) return launch_one<T, OutT, ACT, 64, 1, 4, 2, 128, 2, 8, 128>(p, st);
