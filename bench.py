@@ -40,6 +40,16 @@ def _usable_cores() -> int:
     return max(1, n)
 
 
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown CPU"
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -159,6 +169,8 @@ def main() -> int:
         peak = MFMA_PEAK["fp8" if fp8 else "bf16"]
         roof = {"bound": "mfma", "achieved": gu_flops / k_s / 1e12, "peak": peak / 1e12, "unit": "TFLOP/s"}
     roof["frac"] = roof["achieved"] / roof["peak"]
+    if roof["bound"] == "mfma":   # the other roofline of the same launch, on its algorithmic bytes
+        roof["hbm_frac"] = gu_bytes / k_s / HBM_PEAK
     # HBM bytes per dispatch of this kernel at this workload, from the committed rocprofv3 --pmc summary
     # (FETCH_SIZE + WRITE_SIZE scaled by a copy kernel of known size); None when not profiled
     from flide_amd.rocprof import traffic_for
@@ -194,7 +206,7 @@ def main() -> int:
         med = times[len(times) // 2]
         cpu = {"value": Tc / med, "unit": "tokens/s", "cores": ncores, "kind": "port",
                "sample": f"{len(times)} runs (median) of route+experts on {Tc} of the {cfg.T} tokens, fp32, "
-                         f"torch CPU (transformers' eager Gemma 4 experts loop restated)"}
+                         f"torch CPU (transformers' eager Gemma 4 experts loop restated), {_cpu_model()}"}
 
     rec = {
         "metric": "MoE layer tokens/s @ 26B-A4B shape, bf16 & FP8; % of HBM/MFMA peak",
