@@ -182,3 +182,16 @@ def test_decode_workload_hits_most_experts():
     _, ids = orc.route(d["logits"].numpy(), 8)
     hit = (np.bincount(ids.reshape(-1), minlength=128) > 0).sum()
     assert 115 <= hit <= 128      # ~126 expected at T = 64, k = 8, E = 128
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU: --gpus N > 1 (or a multi-rank launch) exits 2 with a message."""
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    root = Path(__file__).resolve().parent.parent
+    r = subprocess.run([sys.executable, str(root / "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 2
+    assert "one GPU" in r.stderr
