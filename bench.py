@@ -176,6 +176,14 @@ def main() -> int:
     from flide_amd.rocprof import traffic_for
     roof["traffic"] = traffic_for(cfg.name)
     roof["algorithmic_bytes"] = gu_bytes
+    # the whole layer against the same peak: its algorithmic bytes (all hit experts' weights, x and the
+    # router table) for the HBM-bound decode case, its expert FLOPs otherwise; per step of the timed loop
+    if roof["bound"] == "hbm":
+        layer_bytes = n_hit * 3 * cfg.I * cfg.H * bpw + cfg.T * cfg.H * 2 + cfg.E * cfg.H * 2
+        roof["layer"] = {"achieved": layer_bytes / step_s / 1e9, "frac": layer_bytes / step_s / HBM_PEAK,
+                         "bytes": layer_bytes}
+    else:
+        roof["layer"] = {"achieved": cfg.flops / step_s / 1e12, "frac": cfg.flops / step_s / roof["peak"] / 1e12}
     roof["kernel"] = "grouped gate/up + GeGLU (" + ("fp8" if fp8 else "bf16") + f", bm {bm})"
     roof["kernel_us"] = k_s * 1e6
 
