@@ -3,7 +3,7 @@
 // The reference runs one program per expert, each scanning all n pairs (O(E n)). Here two launches do
 // O(n) work in total:
 //   align_count  chunk c of ALIGN_CHUNK pairs -> an LDS histogram -> hist[c][E] in the workspace
-//                (skipped when all pairs fit one chunk: align_place<true> then counts them itself)
+//                (skipped up to ALIGN_FUSED_MAX pairs: one align_place<true> then counts them itself)
 //   align_place  every chunk sums the histograms before it (and all of them, for the padded expert
 //                offsets), then places its pairs in pair order: each wave walks its quarter of the
 //                chunk 64 pairs at a time; lanes with the same expert find each other with log2(E+1)
@@ -18,8 +18,9 @@ namespace {
 
 constexpr int ALIGN_THREADS = 256;
 constexpr int ALIGN_WAVES = ALIGN_THREADS / 64;
-constexpr int ALIGN_PER_WAVE = 1024;  // pairs one wave places per chunk
+constexpr int ALIGN_PER_WAVE = 256;   // pairs one wave places per chunk (two-launch path)
 constexpr int ALIGN_CHUNK = ALIGN_WAVES * ALIGN_PER_WAVE;
+constexpr int ALIGN_FUSED_MAX = 4096;  // up to this many pairs one workgroup counts and places all
 constexpr int ALIGN_MAX_E = 1024;
 
 __global__ __launch_bounds__(ALIGN_THREADS) void align_count(const int* __restrict__ ids, int n,
@@ -55,7 +56,7 @@ __global__ __launch_bounds__(ALIGN_THREADS) void align_place(const int* __restri
 
   const int cbase = c * ALIGN_CHUNK;
   // this wave's pairs: a quarter of the chunk (FUSED: of all n pairs, in 64-pair steps), in pair order
-  const int wper = FUSED ? (n + 4 * 64 - 1) / (4 * 64) * 64 : ALIGN_PER_WAVE;
+  const int wper = FUSED ? (n + ALIGN_WAVES * 64 - 1) / (ALIGN_WAVES * 64) * 64 : ALIGN_PER_WAVE;
   const int wbase = cbase + wave * wper;
   const int wend = min(n, wbase + wper);
   if constexpr (FUSED) {
@@ -77,6 +78,7 @@ __global__ __launch_bounds__(ALIGN_THREADS) void align_place(const int* __restri
     // per-expert totals and the share of earlier chunks
     for (int e = tid; e < E; e += ALIGN_THREADS) {
       int b = 0, tot = 0;
+#pragma unroll 8
       for (int j = 0; j < nchunks; ++j) {
         int v = hist[(long long)j * E + e];
         if (j < c) b += v;
@@ -170,11 +172,12 @@ __global__ __launch_bounds__(ALIGN_THREADS) void align_place(const int* __restri
 
 }  // namespace
 
+// chunks of the two-launch path (1 when one workgroup handles every pair)
+int align_chunks(int n) { return n <= ALIGN_FUSED_MAX ? 1 : (n + ALIGN_CHUNK - 1) / ALIGN_CHUNK; }
+
 extern "C" size_t flide_moe_align_workspace(int n, int E) {
   if (n < 0 || E <= 0) return 0;
-  size_t nchunks = (size_t)(n + ALIGN_CHUNK - 1) / ALIGN_CHUNK;
-  if (nchunks == 0) nchunks = 1;
-  return nchunks * (size_t)E * sizeof(int);
+  return (size_t)align_chunks(n) * (size_t)E * sizeof(int);
 }
 
 extern "C" int flide_moe_align(const int* ids, int n, int E, int bm, int* rows, int* blocks,
@@ -183,10 +186,9 @@ extern "C" int flide_moe_align(const int* ids, int n, int E, int bm, int* rows, 
   if (n < 0 || E <= 0 || E > ALIGN_MAX_E || bm <= 0) return FLIDE_MOE_ERR_ARG;
   if (workspace_bytes < flide_moe_align_workspace(n, E)) return FLIDE_MOE_ERR_WORKSPACE;
   hipStream_t st = (hipStream_t)stream;
-  int nchunks = (n + ALIGN_CHUNK - 1) / ALIGN_CHUNK;
-  if (nchunks == 0) nchunks = 1;
+  const int nchunks = align_chunks(n);
   int* hist = (int*)workspace;
-  if (nchunks == 1) {   // every pair in one chunk: one launch counts and places
+  if (nchunks == 1) {   // one workgroup counts and places every pair
     align_place<true><<<1, ALIGN_THREADS, 0, st>>>(ids, n, E, bm, 1, hist, rows, blocks, used, counts);
     FLIDE_CHECK_LAUNCH();
     return FLIDE_MOE_OK;
