@@ -257,14 +257,19 @@ __global__ __launch_bounds__(RW_THREADS) void quantize_rows_vec_kernel(const u16
     const int c = l + v * 64;
     if (c >= nv) continue;
     const uint32_t w[4] = {raw[v].x, raw[v].y, raw[v].z, raw[v].w};
-    uint32_t packed[2] = {0, 0};
+    float t[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      float t = val(w[i >> 1], i & 1) / sc;   // correctly rounded division
-      t = fminf(fmaxf(t, -448.0f), 448.0f);
-      packed[i >> 2] |= (uint32_t)f32_to_e4m3fn(t) << (8 * (i & 3));
+      t[i] = val(w[i >> 1], i & 1) / sc;   // correctly rounded division
+      t[i] = fminf(fmaxf(t[i], -448.0f), 448.0f);
     }
-    qr[c] = make_uint2(packed[0], packed[1]);
+    // gfx950's packed float32 -> OCP e4m3fn conversion (round to nearest even); on clamped inputs it
+    // gives f32_to_e4m3fn's bytes exactly (checked on every code, every tie and its neighbours)
+    uint32_t lo = __builtin_amdgcn_cvt_pk_fp8_f32(t[0], t[1], 0u, false);
+    lo = __builtin_amdgcn_cvt_pk_fp8_f32(t[2], t[3], lo, true);
+    uint32_t hi = __builtin_amdgcn_cvt_pk_fp8_f32(t[4], t[5], 0u, false);
+    hi = __builtin_amdgcn_cvt_pk_fp8_f32(t[6], t[7], hi, true);
+    qr[c] = make_uint2(lo, hi);
   }
 }
 
