@@ -27,6 +27,7 @@ SIGNATURES: dict[str, list] = {
     "flide_moe_strerror": [_I],
     "flide_moe_version": [],
     "flide_moe_router": [_P, _L, _I, _I, _I, _P, _L, _I, _P, _P, _L, _P, _P],
+    "flide_moe_router_norm": [_P, _L, _I, _I, _I, _P, _P, _L, _I, c_float, _P, _L, _P, _I, _P, _L, _P],
     "flide_moe_route": [_P, _L, _I, _I, _I, _P, _I, _P, _P, _P],
     "flide_moe_align_workspace": [_I, _I],
     "flide_moe_align": [_P, _I, _I, _I, _P, _P, _P, _P, _P, c_size_t, _P],

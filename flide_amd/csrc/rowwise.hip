@@ -404,14 +404,107 @@ extern "C" int flide_moe_quantize_rows(const void* x, long long sx, int M, int K
   return FLIDE_MOE_OK;
 }
 
+// RMSNorm of 16-bit rows into the same type (flide/kernels/pointwise.py:21-36): one wave per row, the
+// row held in registers between the two passes (NV 16-byte chunks per lane), so x is read from memory once.
+template <bool BF16, int WDT, int NV>
+__global__ __launch_bounds__(RW_THREADS) void rms_norm_vec_kernel(const u16* __restrict__ x, long long sx,
+                                                                  const void* __restrict__ w,
+                                                                  u16* __restrict__ y, long long sy, int N,
+                                                                  int T, float eps, int offset) {
+  const int l = threadIdx.x & 63;
+  const long long row = (long long)blockIdx.x * (RW_THREADS / 64) + (threadIdx.x >> 6);
+  if (row >= T) return;
+  const int nv = N / 8;
+  const uint4* xr = (const uint4*)(x + row * sx);
+  uint4 raw[NV];
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int c = l + v * 64;
+    raw[v] = c < nv ? xr[c] : make_uint4(0, 0, 0, 0);
+  }
+  auto val = [](uint32_t u, int hi) {
+    const u16 h = hi ? (u16)(u >> 16) : (u16)(u & 0xffff);
+    return BF16 ? bf16_to_f32(h) : f16_to_f32(h);
+  };
+  auto rnd = [](float f) -> uint32_t { return BF16 ? f32_to_bf16(f) : f32_to_f16(f); };
+  float ss = 0.f;
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const uint32_t u[4] = {raw[v].x, raw[v].y, raw[v].z, raw[v].w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float f = val(u[i >> 1], i & 1);
+      ss += f * f;
+    }
+  }
+  ss = wave_sum(ss);
+  const float inv = rsqrtf(ss / N + eps);
+  uint4* yr = (uint4*)(y + row * sy);
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int c = l + v * 64;
+    if (c >= nv) continue;
+    float wv[8];
+    if constexpr (WDT == FLIDE_F32) {
+      const float4 w0 = ((const float4*)w)[2 * c], w1 = ((const float4*)w)[2 * c + 1];
+      wv[0] = w0.x; wv[1] = w0.y; wv[2] = w0.z; wv[3] = w0.w;
+      wv[4] = w1.x; wv[5] = w1.y; wv[6] = w1.z; wv[7] = w1.w;
+    } else {
+      const uint4 wr = ((const uint4*)w)[c];
+      const uint32_t u[4] = {wr.x, wr.y, wr.z, wr.w};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const u16 h = (i & 1) ? (u16)(u[i >> 1] >> 16) : (u16)(u[i >> 1] & 0xffff);
+        wv[i] = WDT == FLIDE_BF16 ? bf16_to_f32(h) : f16_to_f32(h);
+      }
+    }
+    const uint32_t u[4] = {raw[v].x, raw[v].y, raw[v].z, raw[v].w};
+    uint32_t o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float w0 = offset ? 1.0f + wv[2 * i] : wv[2 * i], w1 = offset ? 1.0f + wv[2 * i + 1] : wv[2 * i + 1];
+      o[i] = rnd(val(u[i], 0) * inv * w0) | (rnd(val(u[i], 1) * inv * w1) << 16);
+    }
+    yr[c] = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+}
+
+template <bool BF16, int WDT>
+void launch_rms_norm_vec(const void* x, long long sx, const void* w, void* y, long long sy, int T, int N,
+                         float eps, int offset, hipStream_t st) {
+  const int per_lane = (N / 8 + 63) / 64;
+  const dim3 grid((T + RW_THREADS / 64 - 1) / (RW_THREADS / 64));
+#define RV(NV) rms_norm_vec_kernel<BF16, WDT, NV><<<grid, RW_THREADS, 0, st>>>( \
+    (const u16*)x, sx, w, (u16*)y, sy, N, T, eps, offset)
+  if (per_lane <= 1) RV(1);
+  else if (per_lane <= 2) RV(2);
+  else if (per_lane <= 4) RV(4);
+  else if (per_lane <= 6) RV(6);
+  else if (per_lane <= 8) RV(8);
+  else RV(16);
+#undef RV
+}
+
 extern "C" int flide_moe_rms_norm(const void* x, long long sx, int x_dtype, const void* w,
                                   int w_dtype, void* y, long long sy, int y_dtype, int T, int N,
                                   float eps, int offset, flide_stream_t stream) {
   if (T < 0 || N <= 0 || !dtype_ok(x_dtype) || !dtype_ok(w_dtype) || !dtype_ok(y_dtype))
     return FLIDE_MOE_ERR_ARG;
   if (T == 0) return FLIDE_MOE_OK;
-  rms_norm_kernel<<<T, RW_THREADS, 0, (hipStream_t)stream>>>(x, sx, x_dtype, w, w_dtype, y, sy,
-                                                             y_dtype, N, eps, offset);
+  hipStream_t st = (hipStream_t)stream;
+  // 16-bit rows into their own type, 16-byte aligned, at most 8192 wide: the vector kernel
+  if (x_dtype != FLIDE_F32 && y_dtype == x_dtype && N % 8 == 0 && N <= 64 * 8 * 16 && sx % 8 == 0 &&
+      sy % 8 == 0 && !(((uintptr_t)x | (uintptr_t)y | (uintptr_t)w) & 15)) {
+#define RN(BF, WD) launch_rms_norm_vec<BF, WD>(x, sx, w, y, sy, T, N, eps, offset, st)
+    const bool bf = x_dtype == FLIDE_BF16;
+    if (w_dtype == FLIDE_F32) { if (bf) RN(true, FLIDE_F32); else RN(false, FLIDE_F32); }
+    else if (w_dtype == FLIDE_BF16) { if (bf) RN(true, FLIDE_BF16); else RN(false, FLIDE_BF16); }
+    else { if (bf) RN(true, FLIDE_F16); else RN(false, FLIDE_F16); }
+#undef RN
+    FLIDE_CHECK_LAUNCH();
+    return FLIDE_MOE_OK;
+  }
+  rms_norm_kernel<<<T, RW_THREADS, 0, st>>>(x, sx, x_dtype, w, w_dtype, y, sy, y_dtype, N, eps, offset);
   FLIDE_CHECK_LAUNCH();
   return FLIDE_MOE_OK;
 }

@@ -72,6 +72,37 @@ def router(x: torch.Tensor, wr: torch.Tensor, wg: torch.Tensor | None = None):
     return logits, gate
 
 
+ROUTER_NORM_MAX_H = 8192   # flide_moe_router_norm's limit (include/flide_moe.h)
+
+
+def router_norm(h: torch.Tensor, norm_w: torch.Tensor, wr: torch.Tensor, eps: float,
+                norm2_w: torch.Tensor | None = None):
+    """Gemma 4's router input fused into the router (an extension; flide/backbones/gemma4/fused.py:234-237
+    runs it as three calls): (logits f32 [T, E], x2 [T, H] or None) for the residual stream h [T, H], with
+    logits = router(rms_norm(h, norm_w), wr) and x2 = rms_norm(h, norm2_w) (pointwise.py:21-49, no offset,
+    rounded to h's dtype). Both norms share one statistic per token, computed once."""
+    dev = _hip.require_gpu(h, norm_w, wr, norm2_w)
+    T, H = h.shape
+    E = wr.shape[0]
+    if H > ROUTER_NORM_MAX_H:   # the fused kernel stages both weights in LDS: the three calls instead
+        from flide_amd.kernels import pointwise as pw
+        logits, _ = router(pw.rms_norm(h, norm_w, eps, offset=False), wr)
+        return logits, (pw.rms_norm(h, norm2_w, eps, offset=False) if norm2_w is not None else None)
+    if h.stride(-1) != 1:
+        h = h.contiguous()
+    wr = wr.contiguous()
+    nw = norm_w.float().contiguous()
+    logits = torch.empty(T, E, device=dev, dtype=torch.float32)
+    x2 = torch.empty_like(h) if norm2_w is not None else None
+    n2 = norm2_w.contiguous() if norm2_w is not None else None
+    if T:
+        _hip.call("flide_moe_router_norm", h.data_ptr(), h.stride(0), T, H, _hip.dtype_code(h.dtype), nw.data_ptr(),
+                  wr.data_ptr(), wr.stride(0), E, float(eps), logits.data_ptr(), logits.stride(0), _hip.ptr(n2),
+                  _hip.dtype_code(n2.dtype) if n2 is not None else 0, _hip.ptr(x2),
+                  x2.stride(0) if x2 is not None else 0, _hip.stream(dev))
+    return logits, x2
+
+
 def route(logits: torch.Tensor, k: int, scale: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
     """(weights [T, k] float32, experts [T, k] int32) from router logits [T, E]: the top k in descending
     order (ties to the lower id), renormalised to sum to one, times each expert's `scale` [E] when given

@@ -57,10 +57,29 @@ const char* flide_moe_version(void);
  * logits[t, e] = sum_h x[t, h] * wr[e, h] and, when wg != NULL, gate[t] = sum_h x[t, h] * wg[h], both
  * summed and stored in float32. x: [T, H] (x_dtype BF16 or F16, row stride sx); wr: [E, H] (same dtype,
  * row stride swr); wg: [H] or NULL; logits: [T, E] float32 (row stride sl); gate: [T] float32.
+ * The K sum's order does not depend on T, so a token's logits are the same bits in any batch.
  */
 int flide_moe_router(const void* x, long long sx, int T, int H, int x_dtype, const void* wr,
                      long long swr, int E, const void* wg, float* logits, long long sl, float* gate,
                      flide_stream_t stream);
+
+/*
+ * Router logits with the router's RMSNorm fused in. Replaces the Gemma 4 glue
+ *   r = pointwise.rms_norm(h, router_norm); logits = moe.router(r, W_r);
+ *   x2 = pointwise.rms_norm(h, pre_feedforward_layernorm_2.weight)
+ * (flide/backbones/gemma4/fused.py:234-237; pointwise.py:21-49 without offset or residual) in one
+ * launch. With inv = rsqrt(mean_h(h^2) + eps) per token: r = round((h * inv) * norm_w), logits = r @ wr^T
+ * summed in float32, and, when x2 != NULL, x2 = round((h * inv) * norm2_w), rounded to h's type.
+ * h: [T, H] (h_dtype BF16 or F16, row stride sh); norm_w: [H] float32; wr: [E, H] (h's type, row stride
+ * swr); logits: [T, E] float32 (row stride sl); norm2_w: [H] (norm2_dtype F32, BF16 or F16) or NULL;
+ * x2: [T, H] in h's type (row stride sx2) or NULL. H <= 8192; H, sh, swr and sx2 multiples of 8; h, wr,
+ * norm_w, norm2_w and x2 16-byte aligned. A token's logits are the same bits whatever T (as
+ * flide_moe_router's, which sums K in the same order).
+ */
+int flide_moe_router_norm(const void* h, long long sh, int T, int H, int h_dtype, const float* norm_w,
+                          const void* wr, long long swr, int E, float eps, float* logits, long long sl,
+                          const void* norm2_w, int norm2_dtype, void* x2, long long sx2,
+                          flide_stream_t stream);
 
 /*
  * Routing. Replaces moe.route + _route_kernel (flide/kernels/moe.py:172-204).

@@ -313,11 +313,13 @@ def test_quantize_experts_matches_rows():
     np.testing.assert_array_equal(q.cpu().view(torch.uint8).numpy(), orc.e4m3fn_encode(rq))
 
 
-def test_router_logits():
-    print("router", flush=True)
+@pytest.mark.parametrize("T,H,E", [(77, 2816, 128), (1100, 2816, 200), (5, 200, 64), (40, 40, 128)])
+def test_router_logits(T, H, E):
+    """Both router tiles (16 x 32 up to 1024 tokens, 64 x 64 above), a partial expert tile (E = 200), fewer
+    32-wide K steps than waves (H = 200: 7 steps over 8 waves) and a partial last step (H = 40)."""
+    print(f"router T={T} H={H} E={E}", flush=True)
     moe = _moe()
-    g = torch.Generator().manual_seed(15)
-    T, H, E = 77, 2816, 128
+    g = torch.Generator().manual_seed(15 + T)
     x = torch.randn(T, H, generator=g).to(torch.bfloat16)
     wr = (torch.randn(E, H, generator=g) * 0.02).to(torch.bfloat16)
     wg = (torch.randn(H, generator=g) * 0.02).to(torch.bfloat16)
@@ -325,6 +327,84 @@ def test_router_logits():
     rl, rg = orc.router(np32(x), np32(wr), np32(wg))
     np.testing.assert_allclose(logits.cpu().numpy(), rl, rtol=1e-5, atol=1e-5)
     np.testing.assert_allclose(gate.cpu().numpy(), rg, rtol=1e-5, atol=1e-5)
+
+
+def test_router_batch_invariant():
+    """A token's logits are the same bits whichever batch it is routed in: the K split over waves is fixed,
+    only the tile changes with T (77 tokens: small tiles; 1100: large tiles), for both router forms."""
+    print("router batch invariance", flush=True)
+    moe = _moe()
+    g = torch.Generator().manual_seed(23)
+    T, H, E = 1100, 2816, 128
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16).to(DEV)
+    wr = (torch.randn(E, H, generator=g) * 0.02).to(torch.bfloat16).to(DEV)
+    nw = (torch.rand(H, generator=g) * 0.1).to(DEV)
+    n2 = (torch.rand(H, generator=g) + 0.5).to(torch.bfloat16).to(DEV)
+    big, _ = moe.router(x, wr)
+    for a, b in ((0, 77), (500, 577), (1090, 1100)):
+        small, _ = moe.router(x[a:b], wr)
+        assert torch.equal(small, big[a:b]), (a, b)
+    bl, bx = moe.router_norm(x, nw, wr, 1e-6, n2)
+    sl, sx = moe.router_norm(x[500:577], nw, wr, 1e-6, n2)
+    assert torch.equal(sl, bl[500:577]) and torch.equal(sx, bx[500:577])
+
+
+@pytest.mark.parametrize("T,E,dt,n2dt", [(77, 128, torch.bfloat16, "same"), (77, 200, torch.bfloat16, "same"),
+                                         (77, 128, torch.float16, "same"), (1100, 200, torch.bfloat16, "same"),
+                                         (5000, 128, torch.bfloat16, torch.float32), (77, 128, torch.bfloat16, None)])
+def test_router_norm_fused(T, E, dt, n2dt):
+    """Gemma's router input fused into the router: logits of rms_norm(h, norm_w) against the router weight,
+    and the experts' input rms_norm(h, norm2_w), from one launch. E = 200: a partial expert tile; T = 1100
+    and 5000: the larger tiles; a float32 norm2 weight; no x2 at all."""
+    print(f"router_norm T={T} E={E} {dt} norm2 {n2dt}", flush=True)
+    moe = _moe()
+    g = torch.Generator().manual_seed(17 + E + T)
+    H, eps = 2816, 1e-6
+    h = (torch.randn(T, H, generator=g) * 3).to(dt)
+    norm_w = torch.rand(H, generator=g) * 0.1 + 0.01                 # float32, as Gemma folds its router scale
+    wr = (torch.randn(E, H, generator=g) * 0.02).to(dt)
+    norm2_w = (torch.rand(H, generator=g) + 0.5).to(dt if n2dt == "same" else (n2dt or dt))
+    logits, x2 = moe.router_norm(h.to(DEV), norm_w.to(DEV), wr.to(DEV), eps, norm2_w.to(DEV) if n2dt else None)
+    odt = "bf16" if dt == torch.bfloat16 else "f16"
+    r = orc.rms_norm(np32(h), norm_w.numpy(), eps, offset=False, dtype=odt)
+    rl, _ = orc.router(r, np32(wr))
+    # r may differ from the float64 statistic's rounding by one ulp in a few elements: |dlogit| < 1e-3
+    np.testing.assert_allclose(logits.cpu().numpy(), rl, rtol=1e-3, atol=1e-3)
+    if n2dt is None:
+        assert x2 is None
+    else:
+        rx = orc.rms_norm(np32(h), np32(norm2_w), eps, offset=False, dtype=odt)
+        np.testing.assert_allclose(np32(x2), rx, rtol=2 ** -7 if dt == torch.bfloat16 else 2 ** -10, atol=1e-7)
+    # and the same as the three separate calls the glue makes today, to the same bar
+    from flide_amd.kernels import pointwise as pw
+    l3, _ = moe.router(pw.rms_norm(h.to(DEV), norm_w.to(DEV), eps, offset=False), wr.to(DEV))
+    np.testing.assert_allclose(logits.cpu().numpy(), l3.cpu().numpy(), rtol=1e-3, atol=1e-3)
+
+
+_NAME = {torch.bfloat16: "bf16", torch.float16: "f16", torch.float32: "f32"}
+
+
+@pytest.mark.parametrize("xdt,wdt,N,offset,ydt,pad", [
+    (torch.bfloat16, torch.float32, 2816, False, None, 0),     # Gemma's router norm: the vector kernel
+    (torch.bfloat16, torch.bfloat16, 2816, True, None, 0),     # Qwen's zero-centred weight
+    (torch.float16, torch.float16, 704, False, None, 0),
+    (torch.bfloat16, torch.bfloat16, 8192, False, None, 24),   # 16 chunks per lane, strided rows
+    (torch.bfloat16, torch.float32, 8200, False, None, 0),     # wider than the vector kernel: scalar kernel
+    (torch.bfloat16, torch.float32, 100, False, None, 0),      # N % 8 != 0: scalar kernel
+    (torch.bfloat16, torch.float32, 2816, False, torch.float32, 0),   # another output type: scalar kernel
+])
+def test_rms_norm(xdt, wdt, N, offset, ydt, pad):
+    print(f"rms_norm {xdt} w {wdt} N={N} offset={offset} y {ydt} pad={pad}", flush=True)
+    from flide_amd.kernels import pointwise as pw
+
+    g = torch.Generator().manual_seed(N + pad)
+    xf = (torch.randn(45, N + pad, generator=g) * 2).to(xdt)
+    x = xf[:, :N]
+    w = (torch.rand(N, generator=g) * 0.5 - (0.25 if offset else -0.01)).to(wdt)
+    y = pw.rms_norm(x.to(DEV) if not pad else xf.to(DEV)[:, :N], w.to(DEV), 1e-6, offset=offset, dtype=ydt)
+    ref = orc.rms_norm(np32(x), np32(w), 1e-6, offset=offset, dtype=_NAME[ydt or xdt])
+    tol = {torch.bfloat16: 2 ** -7, torch.float16: 2 ** -10, torch.float32: 1e-5}[ydt or xdt]
+    np.testing.assert_allclose(np32(y), ref, rtol=tol, atol=1e-6)
 
 
 def test_rms_norm_and_geglu():
