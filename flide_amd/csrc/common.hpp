@@ -74,28 +74,62 @@ FLIDE_DEV float e4m3fn_to_f32(u8 c) {
 // ---------------------------------------------------------------------------------------------------
 // wave64 reductions
 // ---------------------------------------------------------------------------------------------------
+// All-reductions in registers: two DPP butterflies inside each quad (quad_perm [1,0,3,2] and [2,3,0,1]),
+// row_half_mirror and row_mirror inside each row of 16 lanes, then gfx950's v_permlane16_swap and
+// v_permlane32_swap across rows (no LDS round trip). Each step combines a lane's value with its partner's
+// by a commutative operation, so every lane ends with the same bits, and the two outputs of a swap (the
+// lane's own value and its partner's, in an order that depends on the lane) need no select. All 64 lanes
+// must be active.
+FLIDE_DEV int dpp_xor1(int v) { return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, true); }
+FLIDE_DEV int dpp_xor2(int v) { return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, true); }
+FLIDE_DEV int dpp_half_mirror(int v) { return __builtin_amdgcn_mov_dpp(v, 0x141, 0xF, 0xF, true); }
+FLIDE_DEV int dpp_mirror(int v) { return __builtin_amdgcn_mov_dpp(v, 0x140, 0xF, 0xF, true); }
+
+template <typename Op> FLIDE_DEV float wave_reduce(float v, Op op) {
+  v = op(v, __int_as_float(dpp_xor1(__float_as_int(v))));
+  v = op(v, __int_as_float(dpp_xor2(__float_as_int(v))));
+  v = op(v, __int_as_float(dpp_half_mirror(__float_as_int(v))));
+  v = op(v, __int_as_float(dpp_mirror(__float_as_int(v))));
+  const auto s16 = __builtin_amdgcn_permlane16_swap(__float_as_int(v), __float_as_int(v), false, false);
+  v = op(__int_as_float(s16[0]), __int_as_float(s16[1]));
+  const auto s32 = __builtin_amdgcn_permlane32_swap(__float_as_int(v), __float_as_int(v), false, false);
+  return op(__int_as_float(s32[0]), __int_as_float(s32[1]));
+}
+
 FLIDE_DEV float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
+  return wave_reduce(v, [](float a, float b) { return fmaxf(a, b); });
 }
 
 FLIDE_DEV float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+  return wave_reduce(v, [](float a, float b) { return a + b; });
 }
 
-// (value, index) argmax over the wave: larger value wins, the lower index on equal values. Indices
-// of lanes with nothing left carry value -inf and index INT_MAX, so they never win over a real entry.
+// (value, index) argmax over the wave: larger value wins, the lower index on equal values (a total
+// order, so the combination is commutative). Lanes with nothing left carry value -inf and index
+// INT_MAX, so they never win over a real entry.
 FLIDE_DEV void wave_argmax(float& v, int& i) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    float ov = __shfl_xor(v, o, 64);
-    int oi = __shfl_xor(i, o, 64);
-    bool take = (ov > v) || (ov == v && oi < i);
+  auto pick = [](float& v, int& i, float ov, int oi) {
+    const bool take = (ov > v) || (ov == v && oi < i);
     v = take ? ov : v;
     i = take ? oi : i;
+  };
+  pick(v, i, __int_as_float(dpp_xor1(__float_as_int(v))), dpp_xor1(i));
+  pick(v, i, __int_as_float(dpp_xor2(__float_as_int(v))), dpp_xor2(i));
+  pick(v, i, __int_as_float(dpp_half_mirror(__float_as_int(v))), dpp_half_mirror(i));
+  pick(v, i, __int_as_float(dpp_mirror(__float_as_int(v))), dpp_mirror(i));
+  {
+    const auto sv = __builtin_amdgcn_permlane16_swap(__float_as_int(v), __float_as_int(v), false, false);
+    const auto si = __builtin_amdgcn_permlane16_swap(i, i, false, false);
+    v = __int_as_float(sv[0]);
+    i = si[0];
+    pick(v, i, __int_as_float(sv[1]), si[1]);
+  }
+  {
+    const auto sv = __builtin_amdgcn_permlane32_swap(__float_as_int(v), __float_as_int(v), false, false);
+    const auto si = __builtin_amdgcn_permlane32_swap(i, i, false, false);
+    v = __int_as_float(sv[0]);
+    i = si[0];
+    pick(v, i, __int_as_float(sv[1]), si[1]);
   }
 }
 

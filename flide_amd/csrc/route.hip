@@ -346,7 +346,7 @@ __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ lo
   // probabilities of the selected experts, summed in slot order (lane reads of lanes 0..k-1)
   const float my_p = l < k ? expf(my_v - m) / s : 0.f;
   float topsum = 0.f;
-  for (int j = 0; j < k; ++j) topsum += __shfl(my_p, j);
+  for (int j = 0; j < k; ++j) topsum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_p), j));
   if (l < k) {
     float ww = my_p / topsum;
     if (scale) ww *= load_scalar(scale, scale_dtype, my_id);
