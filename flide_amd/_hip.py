@@ -37,6 +37,8 @@ SIGNATURES: dict[str, list] = {
                               _I, _I, _I, _I, _I, _I, _P],
     "flide_moe_quantize_rows": [_P, _L, _I, _I, _I, _P, _L, _P, _P],
     "flide_moe_combine_norm": [_P, _I, _P, _L, _P, _P, _I, _P, _L, _I, _I, _I, _I, c_float, _P],
+    "flide_moe_combine_norm_sandwich": [_P, _I, _P, _L, _P, _P, _P, _L, _P, _P, _I, _P, _P, _L, _P, _L, _I, _I, _I,
+                                        c_float, _P],
     "flide_moe_combine": [_P, _I, _P, _P, _P, _I, _I, _I, _I, _P],
     "flide_moe_rms_norm": [_P, _L, _I, _P, _I, _P, _L, _I, _I, _I, c_float, _I, _P],
     "flide_moe_gated_act": [_P, _L, _P, _L, _P, _L, _I, _I, _I, _I, _P],

@@ -1,6 +1,7 @@
-"""Timing of the steps in front of the MoE layer at the Gemma 4 shape (H 2816, E 128, bf16): the router,
-rms_norm, the reference's three-call glue (rms_norm -> router, rms_norm; flide/backbones/gemma4/fused.py:234-237)
-and the fused router_norm, with torch.mm (hipBLASLt) beside the router for scale.
+"""Timing of the steps on either side of the MoE layer at the Gemma 4 shape (H 2816, E 128, top-8, bf16):
+in front, the router, rms_norm, the reference's three-call glue (rms_norm -> router, rms_norm;
+flide/backbones/gemma4/fused.py:234-237) and the fused router_norm, with torch.mm (hipBLASLt) beside the router
+for scale; behind, combine_norm alone and fused with the post-norm step (combine_norm_sandwich, fused.py:215,224).
 
 Each entry is the mean over 20 replays of a HIP graph holding 20 calls, so one launch of a small kernel
 (about 4-5 us) is part of every figure, as it is inside a captured layer. Prints one JSON line per batch size.
@@ -60,12 +61,21 @@ def run(tokens) -> list[dict]:
             logits, _ = moe.router(pw.rms_norm(h, nw, EPS, offset=False), wr)
             return logits, pw.rms_norm(h, n2, EPS, offset=False)
 
+        y = torch.randn(T * 8, H, device=dev, generator=gen)
+        dense = torch.randn(T, H, device=dev, generator=gen).to(torch.bfloat16)
+        w1, w2, wp, wn = (torch.rand(H, device=dev, generator=gen).to(torch.bfloat16) + 0.5 for _ in range(4))
+        sc = torch.tensor([0.75], device=dev, dtype=torch.bfloat16)
+
         row = {"tokens": T, "unit": "us per call",
                "router": _graph_us(lambda: moe.router(r, wr)),
                "torch_mm_bf16": _graph_us(lambda: torch.mm(r, wr.t())),
                "rms_norm": _graph_us(lambda: pw.rms_norm(h, nw, EPS, offset=False)),
                "three_calls": _graph_us(three),
-               "router_norm": _graph_us(lambda: moe.router_norm(h, nw, wr, EPS, n2))}
+               "router_norm": _graph_us(lambda: moe.router_norm(h, nw, wr, EPS, n2)),
+               "combine_norm": _graph_us(lambda: moe.combine_norm(y, dense, w1, w2, 8, EPS)),
+               "combine_norm_sandwich": _graph_us(
+                   lambda: moe.combine_norm_sandwich(y, dense, w1, w2, 8, EPS, h, wp, sc, wn))}
+        del y
         row = {k: (round(v, 2) if isinstance(v, float) else v) for k, v in row.items()}
         print(json.dumps(row), flush=True)
         out.append(row)

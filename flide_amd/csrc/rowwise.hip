@@ -115,13 +115,30 @@ __global__ __launch_bounds__(RW_THREADS) void combine_norm_kernel(const void* __
 
 // combine_norm, vectorised for the common dtypes (y f32 or bf16; dense, out, w1, w2 bf16) and
 // H <= 4096: every load of the token (k rows of y, dense, both weights) is issued before any sum.
-template <typename YT, int KMAX>
+// With SW, Gemma's next step follows in the same pass (pointwise.sandwich, pointwise.py:214-231): the
+// rounded output d stays in registers and h_out = round((h + d * rsqrt(mean(d^2) + eps) * wp) * s), then,
+// with wn, x_out = round(h_out * rsqrt(mean(h_out^2) + eps) * wn); d itself is not stored.
+struct SandwichArgs {
+  const u16* h;           // the residual stream [T, H]
+  long long sh;
+  const u16* wp;          // post-feed-forward norm weight [H]
+  const void* scale;      // the layer scalar (one element) or null
+  int scale_dtype;
+  const u16* wn;          // next layer's input norm weight [H] or null
+  u16* h_out;
+  long long sho;
+  u16* x_out;
+  long long sxo;
+};
+
+template <typename YT, int KMAX, bool SW = false>
 __global__ __launch_bounds__(RW_THREADS) void combine_norm_bf16_kernel(const YT* __restrict__ y,
                                                                        const u16* __restrict__ dense,
                                                                        long long sd, const u16* __restrict__ w1,
                                                                        const u16* __restrict__ w2,
                                                                        u16* __restrict__ out, long long so,
-                                                                       int H, int k, float eps) {
+                                                                       int H, int k, float eps,
+                                                                       SandwichArgs sw = {}) {
   constexpr int V = 4;  // float4 groups per thread: H <= 256 * 4 * 4
   __shared__ float red[4];
   const long long t = blockIdx.x;
@@ -174,7 +191,62 @@ __global__ __launch_bounds__(RW_THREADS) void combine_norm_bf16_kernel(const YT*
     uint2 o;
     o.x = (uint32_t)f32_to_bf16(o0) | ((uint32_t)f32_to_bf16(o1) << 16);
     o.y = (uint32_t)f32_to_bf16(o2) | ((uint32_t)f32_to_bf16(o3) << 16);
-    ((uint2*)(out + t * so))[c4] = o;
+    if constexpr (SW) {
+      dv[v] = make_float4(bf16_to_f32(o.x & 0xffff), bf16_to_f32(o.x >> 16), bf16_to_f32(o.y & 0xffff),
+                          bf16_to_f32(o.y >> 16));   // d, rounded as the reference stores it
+    } else {
+      ((uint2*)(out + t * so))[c4] = o;
+    }
+  }
+  if constexpr (SW) {
+    float d2 = 0.f;
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      const int c4 = threadIdx.x + v * RW_THREADS;
+      if (c4 >= nv) continue;
+      d2 += dv[v].x * dv[v].x + dv[v].y * dv[v].y + dv[v].z * dv[v].z + dv[v].w * dv[v].w;
+    }
+    const float inv_d = rsqrtf(block_sum(d2, red) / H + eps);
+    const float sc = sw.scale ? load_any(sw.scale, sw.scale_dtype, 0) : 1.f;
+    float h2 = 0.f;
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      const int c4 = threadIdx.x + v * RW_THREADS;
+      if (c4 >= nv) continue;
+      const uint2 hr = ((const uint2*)(sw.h + t * sw.sh))[c4], wr = ((const uint2*)sw.wp)[c4];
+      const float dq[4] = {dv[v].x, dv[v].y, dv[v].z, dv[v].w};
+      const uint32_t hu[2] = {hr.x, hr.y}, wu[2] = {wr.x, wr.y};
+      float hb[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float hh = bf16_to_f32((hu[i >> 1] >> (16 * (i & 1))) & 0xffff);
+        const float ww = bf16_to_f32((wu[i >> 1] >> (16 * (i & 1))) & 0xffff);
+        float r = hh + dq[i] * inv_d * ww;
+        if (sw.scale) r *= sc;
+        hb[i] = bf16_round(r);
+        h2 += hb[i] * hb[i];
+      }
+      dv[v] = make_float4(hb[0], hb[1], hb[2], hb[3]);
+      uint2 o;
+      o.x = (uint32_t)f32_to_bf16(hb[0]) | ((uint32_t)f32_to_bf16(hb[1]) << 16);
+      o.y = (uint32_t)f32_to_bf16(hb[2]) | ((uint32_t)f32_to_bf16(hb[3]) << 16);
+      ((uint2*)(sw.h_out + t * sw.sho))[c4] = o;
+    }
+    if (sw.wn) {
+      const float inv_h = rsqrtf(block_sum(h2, red) / H + eps);
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        const int c4 = threadIdx.x + v * RW_THREADS;
+        if (c4 >= nv) continue;
+        const uint2 wr = ((const uint2*)sw.wn)[c4];
+        uint2 o;
+        o.x = (uint32_t)f32_to_bf16(dv[v].x * inv_h * bf16_to_f32(wr.x & 0xffff)) |
+              ((uint32_t)f32_to_bf16(dv[v].y * inv_h * bf16_to_f32(wr.x >> 16)) << 16);
+        o.y = (uint32_t)f32_to_bf16(dv[v].z * inv_h * bf16_to_f32(wr.y & 0xffff)) |
+              ((uint32_t)f32_to_bf16(dv[v].w * inv_h * bf16_to_f32(wr.y >> 16)) << 16);
+        ((uint2*)(sw.x_out + t * sw.sxo))[c4] = o;
+      }
+    }
   }
 }
 
@@ -483,6 +555,34 @@ void launch_rms_norm_vec(const void* x, long long sx, const void* w, void* y, lo
   else if (per_lane <= 8) RV(8);
   else RV(16);
 #undef RV
+}
+
+extern "C" int flide_moe_combine_norm_sandwich(const void* y, int y_dtype, const void* dense, long long sd,
+                                               const void* w1, const void* w2, const void* h, long long sh,
+                                               const void* w_post, const void* scale, int scale_dtype,
+                                               const void* w_next, void* h_out, long long sho, void* x_out,
+                                               long long sxo, int T, int H, int k, float eps,
+                                               flide_stream_t stream) {
+  if (T < 0 || H <= 0 || k <= 0 || k > 8 || H % 4 || H > 4 * 4 * RW_THREADS) return FLIDE_MOE_ERR_ARG;
+  if (y_dtype != FLIDE_F32 && y_dtype != FLIDE_BF16) return FLIDE_MOE_ERR_ARG;
+  if (scale && !dtype_ok(scale_dtype)) return FLIDE_MOE_ERR_ARG;
+  if (!dense || !w1 || !w2 || !h || !w_post || !h_out || (w_next && !x_out)) return FLIDE_MOE_ERR_ARG;
+  if (sd % 4 || sh % 4 || sho % 4 || (w_next && sxo % 4)) return FLIDE_MOE_ERR_ARG;
+  if (((uintptr_t)y & 15) || (((uintptr_t)dense | (uintptr_t)w1 | (uintptr_t)w2 | (uintptr_t)h | (uintptr_t)w_post |
+                               (uintptr_t)w_next | (uintptr_t)h_out | (uintptr_t)x_out) & 7))
+    return FLIDE_MOE_ERR_ARG;
+  if (T == 0) return FLIDE_MOE_OK;
+  const SandwichArgs sw{(const u16*)h, sh, (const u16*)w_post, scale, scale_dtype, (const u16*)w_next,
+                        (u16*)h_out, sho, (u16*)x_out, sxo};
+  hipStream_t st = (hipStream_t)stream;
+  if (y_dtype == FLIDE_F32)
+    combine_norm_bf16_kernel<float, 8, true><<<T, RW_THREADS, 0, st>>>(
+        (const float*)y, (const u16*)dense, sd, (const u16*)w1, (const u16*)w2, nullptr, 0, H, k, eps, sw);
+  else
+    combine_norm_bf16_kernel<u16, 8, true><<<T, RW_THREADS, 0, st>>>(
+        (const u16*)y, (const u16*)dense, sd, (const u16*)w1, (const u16*)w2, nullptr, 0, H, k, eps, sw);
+  FLIDE_CHECK_LAUNCH();
+  return FLIDE_MOE_OK;
 }
 
 extern "C" int flide_moe_rms_norm(const void* x, long long sx, int x_dtype, const void* w,

@@ -325,6 +325,37 @@ def moe(x: torch.Tensor, w: dict, mm, swiglu) -> torch.Tensor:
     return combine(y, shared, gate, K)
 
 
+def combine_norm_sandwich(y: torch.Tensor, dense: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, k: int,
+                          eps: float, h: torch.Tensor, w_post: torch.Tensor, scale: torch.Tensor | None = None,
+                          w_next: torch.Tensor | None = None):
+    """Gemma 4's combine and the post-feed-forward step in one launch (an extension; the reference runs
+    moe.combine_norm then pointwise.sandwich, flide/backbones/gemma4/fused.py:215,224-225):
+    (h_out, x_out or None) = sandwich(combine_norm(y, dense, w1, w2, k, eps), h, w_post, eps, scale, w_next),
+    with combine_norm's output rounded to bf16 in between as the reference stores it (moe.py:372-395,
+    pointwise.py:214-245). bf16 activations and weights, H <= 4096, k <= 8."""
+    dev = _hip.require_gpu(y, dense, w1, w2, h, w_post, scale, w_next)
+    T, H = dense.shape
+    for t in (dense, h, w1, w2, w_post) + ((w_next,) if w_next is not None else ()):
+        if t.dtype != torch.bfloat16:
+            raise TypeError("combine_norm_sandwich takes bf16 activations and norm weights")
+    h_out = torch.empty_like(h)
+    x_out = torch.empty_like(h) if w_next is not None else None
+    if T:
+        if dense.stride(-1) != 1:
+            dense = dense.contiguous()
+        if h.stride(-1) != 1:
+            h = h.contiguous()
+        y = y.contiguous()
+        w1, w2, w_post = w1.contiguous(), w2.contiguous(), w_post.contiguous()
+        wn = w_next.contiguous() if w_next is not None else None
+        _hip.call("flide_moe_combine_norm_sandwich", y.data_ptr(), _hip.dtype_code(y.dtype), dense.data_ptr(),
+                  dense.stride(0), w1.data_ptr(), w2.data_ptr(), h.data_ptr(), h.stride(0), w_post.data_ptr(),
+                  _hip.ptr(scale), _hip.dtype_code(scale.dtype) if scale is not None else 0, _hip.ptr(wn),
+                  h_out.data_ptr(), h_out.stride(0), _hip.ptr(x_out), x_out.stride(0) if x_out is not None else 0,
+                  T, H, k, float(eps), _hip.stream(dev))
+    return h_out, x_out
+
+
 def combine_norm(y: torch.Tensor, dense: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, k: int,
                  eps: float) -> torch.Tensor:
     """Gemma 4's two feed-forward branches joined: RMSNorm(dense) * w1 + RMSNorm(sum over each token's k

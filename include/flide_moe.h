@@ -164,6 +164,24 @@ int flide_moe_combine_norm(const void* y, int y_dtype, const void* dense, long l
                            int out_dtype, int T, int H, int k, float eps, flide_stream_t stream);
 
 /*
+ * Gemma 4 combine fused with the step after it. Replaces
+ *   d = moe.combine_norm(y, dense, w1, w2, k, eps)                              (moe.py:372-395)
+ *   h_out, x_out = pointwise.sandwich(d, h, w_post, eps, scale=s, w2=w_next)   (pointwise.py:214-245)
+ * as called at flide/backbones/gemma4/fused.py:215,224-225, in one launch: d is rounded to bf16 as the
+ * reference stores it but never written; h_out = round((h + RMS(d) * w_post) * s) (s = *scale, or no
+ * multiply when scale is NULL); with w_next, x_out = round(RMS(h_out) * w_next). float32 math.
+ * y: [T*k, H] F32 or BF16 (contiguous, 16-byte aligned); dense, h, h_out, x_out: [T, H] bf16 (row
+ * strides sd, sh, sho, sxo, multiples of 4); w1, w2, w_post, w_next: [H] bf16; scale: one element of
+ * scale_dtype or NULL; w_next and x_out both NULL to skip x_out. H % 4 == 0, H <= 4096, k <= 8; bf16
+ * arrays 8-byte aligned.
+ */
+int flide_moe_combine_norm_sandwich(const void* y, int y_dtype, const void* dense, long long sd,
+                                    const void* w1, const void* w2, const void* h, long long sh,
+                                    const void* w_post, const void* scale, int scale_dtype,
+                                    const void* w_next, void* h_out, long long sho, void* x_out,
+                                    long long sxo, int T, int H, int k, float eps, flide_stream_t stream);
+
+/*
  * Qwen3.5 combine. Replaces moe.combine + _combine_kernel (flide/kernels/moe.py:256-277):
  * out[t] = sum_{j<k} y[t*k + j] + shared[t] * sigmoid(gate[t]), float32 math, rounded once.
  * y: [T*k, H] (y_dtype); shared: [T, H] contiguous (out_dtype); gate: [T] float32; out: [T, H].

@@ -306,6 +306,22 @@ def combine_norm(y, dense, w1, w2, k: int, eps: float, dtype: str = "bf16") -> n
     return _round(a + b, dtype)
 
 
+def sandwich(d, h, w1, eps: float, scale=None, w2=None, dtype: str = "bf16"):
+    """flide/kernels/pointwise.py:213-245 (Gemma 4's post-norm step): h_out = (h + RMS(d) * w1) * scale,
+    rounded once to `dtype`; with w2, x = RMS(h_out) * w2 of the rounded h_out, rounded once. Returns
+    (h_out, x or None)."""
+    d = np.asarray(d, np.float64)
+    N = d.shape[-1]
+    r = np.asarray(h, np.float64) + d / np.sqrt((d * d).sum(-1, keepdims=True) / N + eps) * np.asarray(w1, np.float64)
+    if scale is not None:
+        r = r * float(np.asarray(scale, np.float64).reshape(-1)[0])
+    hb = _round(r, dtype)
+    if w2 is None:
+        return hb, None
+    hf = hb.astype(np.float64)
+    return hb, _round(hf / np.sqrt((hf * hf).sum(-1, keepdims=True) / N + eps) * np.asarray(w2, np.float64), dtype)
+
+
 def combine(y, shared, gate, k: int, dtype: str = "bf16") -> np.ndarray:
     """flide/kernels/moe.py:256-277: sum_j y[t*k + j] + shared[t] * sigmoid(gate[t]), rounded once."""
     sh = np.asarray(shared, np.float64)

@@ -269,6 +269,37 @@ def test_combine_norm():
     np.testing.assert_allclose(np32(out), ref, rtol=2 ** -7, atol=1e-6)
 
 
+@pytest.mark.parametrize("ydt,scale,nxt", [(torch.float32, True, True), (torch.bfloat16, False, True),
+                                            (torch.float32, True, False)])
+def test_combine_norm_sandwich(ydt, scale, nxt):
+    """combine_norm and Gemma's following post-norm step (pointwise.sandwich) in one launch."""
+    print(f"combine_norm_sandwich y {ydt} scale={scale} next={nxt}", flush=True)
+    moe = _moe()
+    g = torch.Generator().manual_seed(13)
+    T, H, k, eps = 37, 2816, 8, 1e-6
+    y = torch.randn(T * k, H, generator=g).to(ydt)
+    dense = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    w1, w2, wp, wn = ((torch.rand(H, generator=g) + 0.5).to(torch.bfloat16) for _ in range(4))
+    h = (torch.randn(T, H, generator=g) * 3).to(torch.bfloat16)
+    s = torch.tensor([0.75], dtype=torch.bfloat16)
+    dev = [t.to(DEV) for t in (y, dense, w1, w2, h, wp, s, wn)]
+    h_out, x_out = moe.combine_norm_sandwich(dev[0], dev[1], dev[2], dev[3], k, eps, dev[4], dev[5],
+                                             dev[6] if scale else None, dev[7] if nxt else None)
+    assert (x_out is None) == (not nxt)
+    # the oracle end to end: combine_norm rounded to bf16 (as the reference stores d), then sandwich
+    d = orc.combine_norm(np32(y), np32(dense), np32(w1), np32(w2), k, eps)
+    rh, rx = orc.sandwich(d, np32(h), np32(wp), eps, np32(s) if scale else None, np32(wn) if nxt else None)
+    np.testing.assert_allclose(np32(h_out), rh, rtol=2 ** -7, atol=2 ** -7)
+    if nxt:
+        np.testing.assert_allclose(np32(x_out), rx, rtol=2 ** -6, atol=2 ** -7)
+    # the second phase alone: the oracle's sandwich of this library's own combine_norm output, to one ulp
+    dg = np32(moe.combine_norm(dev[0], dev[1], dev[2], dev[3], k, eps))
+    gh, gx = orc.sandwich(dg, np32(h), np32(wp), eps, np32(s) if scale else None, np32(wn) if nxt else None)
+    np.testing.assert_allclose(np32(h_out), gh, rtol=2 ** -7, atol=1e-6)
+    if nxt:
+        np.testing.assert_allclose(np32(x_out), gx, rtol=2 ** -6, atol=1e-6)
+
+
 def test_combine_qwen():
     print("combine", flush=True)
     moe = _moe()

@@ -255,6 +255,48 @@ def test_combine_norm_matches_gemma4_rmsnorm():
         np.testing.assert_allclose(rn, n1(dense).numpy(), rtol=1e-5, atol=1e-6)
 
 
+def test_sandwich_matches_gemma4_decoder_layer():
+    """pointwise.sandwich is the tail of transformers' Gemma4TextDecoderLayer (no per-layer input):
+    (residual + post_feedforward_layernorm(d)) * layer_scalar, then the next layer's input_layernorm."""
+    from transformers.models.gemma4.modeling_gemma4 import Gemma4RMSNorm
+
+    torch.manual_seed(5)
+    T, H, eps = 7, 40, 1e-6
+    post, nxt = Gemma4RMSNorm(H, eps=eps), Gemma4RMSNorm(H, eps=eps)
+    with torch.no_grad():
+        post.weight.uniform_(0.5, 1.5)
+        nxt.weight.uniform_(0.5, 1.5)
+    d, h, s = torch.randn(T, H), torch.randn(T, H) * 3, torch.tensor([0.7])
+    with torch.no_grad():
+        ref_h = (h + post(d)) * s
+        ref_x = nxt(ref_h)
+    got_h, got_x = orc.sandwich(d.numpy(), h.numpy(), post.weight.detach().numpy(), eps, s.numpy(),
+                                nxt.weight.detach().numpy(), "fp32")
+    np.testing.assert_allclose(got_h, ref_h.numpy(), rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(got_x, ref_x.numpy(), rtol=1e-5, atol=1e-6)
+
+
+def test_sandwich_invariants():
+    rng = np.random.default_rng(6)
+    T, H = 5, 64
+    d = rng.standard_normal((T, H))
+    h = orc.bf16_round(rng.standard_normal((T, H)).astype(np.float32))
+    w1, w2 = rng.uniform(0.5, 1.5, H), rng.uniform(0.5, 1.5, H)
+    # RMS(d) is scale-free: with eps = 0, d and 2 d give the same bits
+    a = orc.sandwich(d, h, w1, 0.0, None, w2)
+    b = orc.sandwich(2 * d, h, w1, 0.0, None, w2)
+    np.testing.assert_array_equal(a[0], b[0])
+    np.testing.assert_array_equal(a[1], b[1])
+    # a zero post-norm weight leaves the (bf16) residual exactly; the layer scalar multiplies it
+    np.testing.assert_array_equal(orc.sandwich(d, h, np.zeros(H), 1e-6)[0], h)
+    np.testing.assert_array_equal(orc.sandwich(d, h, np.zeros(H), 1e-6, np.array([2.0]))[0], 2 * h)
+    # the next norm with unit weight has unit RMS up to one bf16 rounding
+    _, x = orc.sandwich(d, h, w1, 1e-12, None, np.ones(H))
+    rms = np.sqrt((x.astype(np.float64) ** 2).mean(-1))
+    np.testing.assert_allclose(rms, 1.0, atol=2 ** -8)
+    assert orc.sandwich(d, h, w1, 1e-6)[1] is None
+
+
 def test_combine_qwen_closed_form():
     rng = np.random.default_rng(4)
     T, H, k = 5, 16, 3
