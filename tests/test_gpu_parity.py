@@ -458,6 +458,40 @@ def test_rms_norm_and_geglu():
 # --------------------------------------------------------------------------------------------------
 # whole layer
 # --------------------------------------------------------------------------------------------------
+def test_moe_qwen_end_to_end():
+    """Qwen3.5-MoE's feed-forward through moe.moe (moe.py:356-369): router with the shared-expert gate,
+    route, experts with SwiGLU fused, the backbone's own products for the shared expert, combine."""
+    print("moe qwen", flush=True)
+    from flide_amd.kernels import pointwise as pw
+
+    moe = _moe()
+    g = torch.Generator().manual_seed(21)
+    T, H, E, k, I, SI = 33, 2048, 64, 8, 512, 512
+    bf = torch.bfloat16
+    x = torch.randn(T, H, generator=g).to(bf)
+    w = {"router": (torch.randn(E, H, generator=g) * 0.05).to(bf), "shared_gate": (torch.randn(1, H, generator=g) * 0.05).to(bf),
+         "experts": (torch.randn(E, 2 * I, H, generator=g) * 0.03).to(bf),
+         "experts_down": (torch.randn(E, H, I, generator=g) * 0.03).to(bf),
+         "shared_gate_up": (torch.randn(2 * SI, H, generator=g) * 0.03).to(bf),
+         "shared_down": (torch.randn(H, SI, generator=g) * 0.03).to(bf)}
+    wd = {kk: v.to(DEV) for kk, v in w.items()}
+    wd.update({"topk": k, "inter": I, "shared_inter": SI})
+
+    def mm(a, b):   # the backbone's product: a [T, in] x b [out, in]^T
+        return torch.matmul(a, b.t().contiguous())
+
+    out = moe.moe(x.to(DEV), wd, mm, pw.swiglu)
+    # the same steps, each checked on its own
+    logits, gate = moe.router(x.to(DEV), wd["router"], wd["shared_gate"].reshape(-1))
+    top, ids = moe.route(logits, k)
+    rtop, rids = orc.route(logits.cpu().numpy(), k)
+    np.testing.assert_array_equal(ids.cpu().numpy(), rids)
+    shared = mm(pw.swiglu(mm(x.to(DEV), wd["shared_gate_up"]), SI), wd["shared_down"])
+    ry = orc.experts(np32(x), np32(w["experts"]), np32(w["experts_down"]), rtop, rids, I, "swiglu", "bf16")
+    ref = orc.combine(ry, np32(shared), gate.cpu().numpy(), k)
+    assert_close(np32(out), ref, REL_BF16, "moe qwen")
+
+
 def test_layer_cfg1_route_experts_combine():
     print("layer cfg1", flush=True)
     moe = _moe()
