@@ -492,6 +492,51 @@ def test_moe_qwen_end_to_end():
     assert_close(np32(out), ref, REL_BF16, "moe qwen")
 
 
+def test_load_experts_fp8(tmp_path):
+    """Expert weights from checkpoints into the FP8 path: a 16-bit checkpoint is quantised on the device as
+    it is read (the same bytes and scales as quantize_experts and the oracle); a float8 checkpoint in the
+    per-expert layout, with scales in another shard, is taken as stored and runs through experts()."""
+    print("load experts fp8", flush=True)
+    from safetensors.torch import save_file
+
+    from flide_amd import load
+
+    moe = _moe()
+    g = torch.Generator().manual_seed(31)
+    E, I, H, T, k = 8, 192, 512, 40, 4
+    gu16 = (torch.randn(E, 2 * I, H, generator=g) * 0.05).to(torch.bfloat16)
+    dn16 = (torch.randn(E, H, I, generator=g) * 0.05).to(torch.bfloat16)
+    a = tmp_path / "bf16"
+    a.mkdir()
+    save_file({"e.gate_up_proj": gu16, "e.down_proj": dn16}, str(a / "model.safetensors"))
+    w = load.experts(str(a), "e", DEV, fp8=True)
+    q, sc = moe.quantize_experts(gu16.to(DEV))
+    assert torch.equal(w["experts"].view(torch.uint8), q.view(torch.uint8)) and torch.equal(w["experts_scale"], sc)
+    rq, rs = orc.quantize_experts(np32(dn16))
+    np.testing.assert_array_equal(w["experts_down_scale"].cpu().numpy(), rs)
+    np.testing.assert_array_equal(w["experts_down"].cpu().view(torch.uint8).numpy(), orc.e4m3fn_encode(rq))
+
+    b = tmp_path / "fp8"
+    b.mkdir()
+    sh1, sh2 = {}, {}
+    for j in range(E):   # as a float8 export stores them: per expert, the scales in the first shard
+        for n, qt, st in (("gate", w["experts"][j, :I], w["experts_scale"][j, :I]),
+                          ("up", w["experts"][j, I:], w["experts_scale"][j, I:]),
+                          ("down", w["experts_down"][j], w["experts_down_scale"][j])):
+            sh2[f"m.experts.{j}.{n}_proj.weight"] = qt.cpu().contiguous()
+            sh1[f"m.experts.{j}.{n}_proj.weight_scale"] = st.cpu().reshape(-1, 1).contiguous()
+    save_file(sh1, str(b / "model-00001-of-00002.safetensors"))
+    save_file(sh2, str(b / "model-00002-of-00002.safetensors"))
+    w8 = load.experts(str(b), "m.experts", DEV, fp8=True)
+    assert torch.equal(w8["experts"].view(torch.uint8), w["experts"].view(torch.uint8))
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    top, ids = moe.route(torch.randn(T, E, generator=g).to(DEV), k)
+    y = moe.experts(x.to(DEV), w8, top, ids, _gelu_act)
+    ref = orc.experts_fp8(np32(x), np32(w8["experts"]), w8["experts_scale"].cpu().numpy(), np32(w8["experts_down"]),
+                          w8["experts_down_scale"].cpu().numpy(), top.cpu().numpy(), ids.cpu().numpy(), I, "geglu")
+    assert_close(np32(y), ref, REL_FP8, "experts from a float8 checkpoint")
+
+
 def test_layer_cfg1_route_experts_combine():
     print("layer cfg1", flush=True)
     moe = _moe()
