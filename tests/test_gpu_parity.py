@@ -537,6 +537,93 @@ def test_load_experts_fp8(tmp_path):
     assert_close(np32(y), ref, REL_FP8, "experts from a float8 checkpoint")
 
 
+@pytest.mark.parametrize("fp8", [False, True])
+def test_graph_replays_match_eager(fp8):
+    """The Gemma layer captured once into a HIP graph (fused router_norm -> route -> experts ->
+    combine_norm_sandwich), replayed three times on new inputs written between replays by eager work: every
+    replay gives the bits of an eager run on the same inputs."""
+    print(f"graph replays fp8={fp8}", flush=True)
+    moe = _moe()
+    g = torch.Generator().manual_seed(41)
+    T, H, E, k, I, eps = 48, 512, 16, 4, 128, 1e-6
+    bf = torch.bfloat16
+    w = {"experts": (torch.randn(E, 2 * I, H, generator=g) * 0.05).to(bf).to(DEV),
+         "experts_down": (torch.randn(E, H, I, generator=g) * 0.05).to(bf).to(DEV), "inter": I, "topk": k}
+    if fp8:
+        w["experts"], w["experts_scale"] = moe.quantize_experts(w["experts"])
+        w["experts_down"], w["experts_down_scale"] = moe.quantize_experts(w["experts_down"])
+    wr = (torch.randn(E, H, generator=g) * 0.05).to(bf).to(DEV)
+    nw = (torch.rand(H, generator=g) * 0.1).to(DEV)
+    n1, n2, n3, n4, n5 = ((torch.rand(H, generator=g) + 0.5).to(bf).to(DEV) for _ in range(5))
+    scale = (torch.rand(E, generator=g) + 0.5).to(bf).to(DEV)
+    ls = torch.tensor([0.8], dtype=bf, device=DEV)
+    h = torch.empty(T, H, dtype=bf, device=DEV)
+    dense = torch.empty(T, H, dtype=bf, device=DEV)
+
+    def layer():
+        logits, x2 = moe.router_norm(h, nw, wr, eps, n1)
+        top, ids = moe.route(logits, k, scale)
+        y = moe.experts(x2, w, top, ids, _gelu_act)
+        return moe.combine_norm_sandwich(y, dense, n2, n3, k, eps, h, n4, ls, n5)
+
+    def new_inputs(seed):
+        gg = torch.Generator().manual_seed(seed)
+        h.copy_((torch.randn(T, H, generator=gg) * 2).to(bf))
+        dense.copy_(torch.randn(T, H, generator=gg).to(bf))
+
+    new_inputs(0)
+    layer()   # outside capture first (the activation callable is recognised here)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out_h, out_x = layer()
+    for rep in range(1, 4):
+        new_inputs(rep)
+        graph.replay()
+        torch.cuda.synchronize()
+        got_h, got_x = out_h.clone(), out_x.clone()
+        ref_h, ref_x = layer()
+        torch.cuda.synchronize()
+        assert torch.equal(got_h, ref_h) and torch.equal(got_x, ref_x), f"replay {rep}"
+
+
+def test_graph_replays_match_eager_qwen():
+    """Qwen's moe() (torch products for the shared expert inside) under the same capture and replay check."""
+    print("graph replays qwen", flush=True)
+    from flide_amd.kernels import pointwise as pw
+
+    moe = _moe()
+    g = torch.Generator().manual_seed(42)
+    T, H, E, k, I, SI = 40, 512, 16, 4, 128, 128
+    bf = torch.bfloat16
+    w = {"router": (torch.randn(E, H, generator=g) * 0.05).to(bf), "shared_gate": (torch.randn(1, H, generator=g) * 0.05).to(bf),
+         "experts": (torch.randn(E, 2 * I, H, generator=g) * 0.05).to(bf),
+         "experts_down": (torch.randn(E, H, I, generator=g) * 0.05).to(bf),
+         "shared_gate_up": (torch.randn(2 * SI, H, generator=g) * 0.05).to(bf),
+         "shared_down": (torch.randn(H, SI, generator=g) * 0.05).to(bf)}
+    w = {kk: v.to(DEV) for kk, v in w.items()}
+    w.update({"topk": k, "inter": I, "shared_inter": SI})
+    x = torch.empty(T, H, dtype=bf, device=DEV)
+
+    def mm(a, b):
+        return torch.matmul(a, b.t().contiguous())
+
+    x.copy_(torch.randn(T, H, generator=g).to(bf))
+    moe.moe(x, w, mm, pw.swiglu)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = moe.moe(x, w, mm, pw.swiglu)
+    for rep in range(3):
+        x.copy_(torch.randn(T, H, generator=g).to(bf))
+        graph.replay()
+        torch.cuda.synchronize()
+        got = out.clone()
+        ref = moe.moe(x, w, mm, pw.swiglu)
+        torch.cuda.synchronize()
+        assert torch.equal(got, ref), f"replay {rep}"
+
+
 def test_layer_cfg1_route_experts_combine():
     print("layer cfg1", flush=True)
     moe = _moe()
