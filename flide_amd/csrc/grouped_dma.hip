@@ -107,11 +107,22 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void grouped_dma(Group
   // blocks of one expert and all their column tiles) and chunk c goes to XCD c % 8, so each XCD's
   // workgroups reuse the chunk's rows and weight tiles from that XCD's L2, and the dead items at the
   // end of the static grid spread over all XCDs. The host rounds the grid to a multiple of 8 * CH.
+  // Inside a chunk the 16-bit gated (gate/up) product runs column-tile major, so the blocks that share a
+  // weight tile start back to back (at 8192 tokens: 16% less HBM fetch, 4-5% faster); the plain (down)
+  // products and the float8 ones run block major, which measured faster for them.
   const int CH = p.ntn * XCD_CHUNK_BLOCKS;
   const int b = blockIdx.x;
   const int j = b >> 3;
-  const int widx = ((j / CH) * 8 + (b & 7)) * CH + j % CH;
-  const int pm = widx / p.ntn, pn = widx % p.ntn;
+  const int chunk = (j / CH) * 8 + (b & 7), within = j % CH;
+  int pm, pn;
+  if constexpr (ACT != ACT_NONE && !FP8) {
+    pm = chunk * XCD_CHUNK_BLOCKS + within % XCD_CHUNK_BLOCKS;
+    pn = within / XCD_CHUNK_BLOCKS;
+  } else {
+    const int widx = chunk * CH + within;
+    pm = widx / p.ntn;
+    pn = widx % p.ntn;
+  }
   if (pm >= p.nbm || pm * BM >= *p.used) return;
   const long long e = p.blocks[pm];
   for (int r = tid; r < BM; r += NW * 64) {
