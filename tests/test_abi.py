@@ -98,6 +98,25 @@ def test_bad_arguments_are_rejected_before_any_launch(lib):
                                  704, null, 1, 16, 0, null, 0, null) == 1
     # combine_norm: H not a multiple of 4
     assert lib.flide_moe_combine_norm(null, 0, null, 10, null, null, 1, null, 10, 1, 3, 10, 2, 1e-6, null) == 1
+    # router_norm: H past the LDS staging limit, a misaligned norm weight, an x2 with no norm2 weight
+    a16 = ctypes.c_void_p(256)
+    rn = [a16, 8200, 4, 8200, 1, a16, a16, 8200, 128, 1e-6, a16, 128, null, 0, null, 0, null]
+    assert lib.flide_moe_router_norm(*rn) == 1
+    rn[1], rn[3], rn[7] = 2816, 2816, 2816
+    rn[5] = ctypes.c_void_p(260)
+    assert lib.flide_moe_router_norm(*rn) == 1
+    rn[5] = a16
+    rn[14] = a16                                                      # x2 without norm2_w
+    assert lib.flide_moe_router_norm(*rn) == 1
+    # combine_norm_sandwich: k past 8, H past 4096, a missing residual
+    sw = [a16, 0, a16, 2816, a16, a16, a16, 2816, a16, null, 0, null, a16, 2816, null, 0, 4, 2816, 9, 1e-6, null]
+    assert lib.flide_moe_combine_norm_sandwich(*sw) == 1
+    sw[18], sw[17] = 8, 4100
+    assert lib.flide_moe_combine_norm_sandwich(*sw) == 1
+    sw[17], sw[6] = 2816, null
+    assert lib.flide_moe_combine_norm_sandwich(*sw) == 1
+    sw[6], sw[16] = a16, 0                                            # T == 0: nothing to do
+    assert lib.flide_moe_combine_norm_sandwich(*sw) == 0
 
 
 def test_signatures_match_the_reference():

@@ -624,6 +624,30 @@ def test_graph_replays_match_eager_qwen():
         assert torch.equal(got, ref), f"replay {rep}"
 
 
+def test_empty_batches():
+    """T = 0 through every entry point on the path: empty outputs of the right shapes, no launch."""
+    print("empty batches", flush=True)
+    from flide_amd.kernels import pointwise as pw
+
+    moe = _moe()
+    H, E, k, bf = 256, 16, 4, torch.bfloat16
+    x = torch.empty(0, H, dtype=bf, device=DEV)
+    wr = torch.randn(E, H, device=DEV).to(bf)
+    nw = torch.rand(H, device=DEV)
+    wb = torch.rand(H, device=DEV).to(bf)
+    logits, gate = moe.router(x, wr, wb)
+    assert logits.shape == (0, E) and gate.shape == (0, 1)
+    lg, x2 = moe.router_norm(x, nw, wr, 1e-6, wb)
+    assert lg.shape == (0, E) and x2.shape == (0, H)
+    top, ids = moe.route(lg, k)
+    assert top.shape == (0, k) and ids.shape == (0, k)
+    assert pw.rms_norm(x, wb, 1e-6, offset=False).shape == (0, H)
+    y = torch.empty(0, H, device=DEV)
+    assert moe.combine_norm(y, x, wb, wb, k, 1e-6).shape == (0, H)
+    ho, xo = moe.combine_norm_sandwich(y, x, wb, wb, k, 1e-6, x, wb, None, wb)
+    assert ho.shape == (0, H) and xo.shape == (0, H)
+
+
 def test_layer_cfg1_route_experts_combine():
     print("layer cfg1", flush=True)
     moe = _moe()
