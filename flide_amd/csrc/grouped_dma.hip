@@ -372,12 +372,14 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void grouped_dma(Group
   }
 }
 
-// Tiles (default BN = 256 weight rows). Two workgroups per CU matter more than deeper rings or larger
-// tiles here (measured: the one-workgroup variants lose 15-40% on gfx950), so the ring fits in 80 KB:
+// Tiles (default BN = 256 weight rows). Two waves per SIMD matter more than deeper rings or larger
+// tiles here (measured: variants with one wave per SIMD lose 15-40% on gfx950; rings of 4-6 stages
+// were slower too): either two 4-wave workgroups per CU, or one 8-wave workgroup:
 //  bm 256 (16-bit): 1 x 4 waves of 256 x 64, 64-byte stage rows, 4 stages = 128 KB, one workgroup per CU;
 //     the waves share all 256 rows, so a block's padded tail costs no MFMA time
-//  bm 128 (16-bit): 2 x 2 waves of 64 x 128, 64-byte stage rows, 3 stages = 72 KB, two workgroups per CU;
-//     the plain (down) product: 2 x 4 waves of 64 x 64 in one 512-thread workgroup (645 -> 598 us)
+//  bm 128 (16-bit): 2 x 4 waves of 64 x 64 in one 512-thread workgroup, 3 stages. Gated (gate/up):
+//     128-byte stage rows (144 KB), 4-10% faster than two workgroups of 2 x 2 waves with 64-byte rows
+//     at 4096-16384 tokens; plain (down): 64-byte rows (72 KB; 645 -> 598 us against 2 x 2 waves)
 //  bm 64  (16-bit): 1 x 4 waves of 64 x 64, 64-byte stage rows, 3 stages = 60 KB, two workgroups per CU
 //  float8 (128-byte stage rows, one 128-wide MFMA step): bm 128 and 64 with BN = 128 and 2 stages
 //     (64 / 48 KB, two or three workgroups per CU); the bm-128 plain (down) product in 8 waves of
@@ -421,9 +423,9 @@ int launch_dma(GroupArgs& p, int bm, hipStream_t st) {
       else return launch_one<T, OutT, ACT, 32, 2, 2, 3, 128, 3, 4, 64>(p, st);
     }
     if (bm == 256) return launch_one<T, OutT, ACT, 256, 1, 4, 4, 64, 1, 2>(p, st);
-    if (bm == 128) {   // plain (down) products: 8 waves of 64 x 64, two per SIMD within one workgroup
+    if (bm == 128) {   // 8 waves of 64 x 64, two per SIMD within one workgroup
       if constexpr (ACT == ACT_NONE) return launch_one<T, OutT, ACT, 128, 2, 4, 3, 64, 1, 4>(p, st);
-      else return launch_one<T, OutT, ACT, 128, 2, 2, 3, 64, 2, 4>(p, st);
+      else return launch_one<T, OutT, ACT, 128, 2, 4, 3, 128, 1, 4>(p, st);
     }
     if (bm == 64) return launch_one<T, OutT, ACT, 64, 1, 4, 3, 64, 2, 8>(p, st);
   }
