@@ -107,15 +107,15 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void grouped_dma(Group
   // blocks of one expert and all their column tiles) and chunk c goes to XCD c % 8, so each XCD's
   // workgroups reuse the chunk's rows and weight tiles from that XCD's L2, and the dead items at the
   // end of the static grid spread over all XCDs. The host rounds the grid to a multiple of 8 * CH.
-  // Inside a chunk the 16-bit gated (gate/up) product runs column-tile major, so the blocks that share a
-  // weight tile start back to back (at 8192 tokens: 16% less HBM fetch, 4-5% faster); the plain (down)
-  // products and the float8 ones run block major, which measured faster for them.
+  // Inside a chunk the gated (gate/up) products run column-tile major, so the blocks that share a weight
+  // tile start back to back (16-bit at 8192 tokens: 16% less HBM fetch, 4-5% faster); the plain (down)
+  // products run block major, which measured 5% faster for them.
   const int CH = p.ntn * XCD_CHUNK_BLOCKS;
   const int b = blockIdx.x;
   const int j = b >> 3;
   const int chunk = (j / CH) * 8 + (b & 7), within = j % CH;
   int pm, pn;
-  if constexpr (ACT != ACT_NONE && !FP8) {
+  if constexpr (ACT != ACT_NONE) {
     pm = chunk * XCD_CHUNK_BLOCKS + within % XCD_CHUNK_BLOCKS;
     pn = within / XCD_CHUNK_BLOCKS;
   } else {
@@ -381,9 +381,11 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void grouped_dma(Group
 //     128-byte stage rows (144 KB), 4-10% faster than two workgroups of 2 x 2 waves with 64-byte rows
 //     at 4096-16384 tokens; plain (down): 64-byte rows (72 KB; 645 -> 598 us against 2 x 2 waves)
 //  bm 64  (16-bit): 1 x 4 waves of 64 x 64, 64-byte stage rows, 3 stages = 60 KB, two workgroups per CU
-//  float8 (128-byte stage rows, one 128-wide MFMA step): bm 128 and 64 with BN = 128 and 2 stages
-//     (64 / 48 KB, two or three workgroups per CU); the bm-128 plain (down) product in 8 waves of
-//     64 x 32 (375 -> 290 us at 4096 tokens); bm 256: 2 stages = 128 KB
+//  float8 (128-byte stage rows, one 128-wide MFMA step): bm 64 with BN = 128 and 2 stages (48 KB, three
+//     workgroups per CU); bm 128 in 8-wave workgroups: the plain (down) product 64 x 32 per wave, 2
+//     stages (375 -> 290 us at 4096 tokens), the gated (gate/up) product 64 x 64 per wave with BN = 256
+//     and 3 stages (144 KB; 5-10% faster than 2 x 2 waves of BN 128 at 4096-16384 tokens); bm 256:
+//     2 stages = 128 KB
 //  bm 32 (decode): 128-byte stage rows, 3 stages. 16-bit: BN = 64 (gated 2 x 2 waves, plain 1 x 4),
 //     36 KB, three workgroups per CU; float8: 1 x 4 waves, BN = 128, 60 KB. Weight-streaming bound:
 //     whole 128-byte lines per row and stage read measurably faster than the half-line pairs of the
@@ -412,9 +414,9 @@ int launch_dma(GroupArgs& p, int bm, hipStream_t st) {
   if constexpr (FP8) {
     if (bm == 32) return launch_one<T, OutT, ACT, 32, 1, 4, 3, 128, 2, 8, 128>(p, st);
     if (bm == 256) return launch_one<T, OutT, ACT, 256, 1, 4, 2, 128, 1, 2>(p, st);
-    if (bm == 128) {   // the plain (down) product: 8 waves of 64 x 32
+    if (bm == 128) {   // 8 waves: down 64 x 32 each (BN 128), gate/up 64 x 64 each (BN 256, 3 stages)
       if constexpr (ACT == ACT_NONE) return launch_one<T, OutT, ACT, 128, 2, 4, 2, 128, 2, 4, 128>(p, st);
-      else return launch_one<T, OutT, ACT, 128, 2, 2, 2, 128, 2, 4, 128>(p, st);
+      else return launch_one<T, OutT, ACT, 128, 2, 4, 3, 128, 1, 4, 256>(p, st);
     }
     if (bm == 64) return launch_one<T, OutT, ACT, 64, 1, 4, 2, 128, 2, 8, 128>(p, st);
   } else {
