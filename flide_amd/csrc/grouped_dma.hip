@@ -380,7 +380,9 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void grouped_dma(Group
 //  bm 128 (16-bit): 2 x 4 waves of 64 x 64 in one 512-thread workgroup, 3 stages. Gated (gate/up):
 //     128-byte stage rows (144 KB), 4-10% faster than two workgroups of 2 x 2 waves with 64-byte rows
 //     at 4096-16384 tokens; plain (down): 64-byte rows (72 KB; 645 -> 598 us against 2 x 2 waves)
-//  bm 64  (16-bit): 1 x 4 waves of 64 x 64, 64-byte stage rows, 3 stages = 60 KB, two workgroups per CU
+//  bm 64  (16-bit): 128-byte stage rows, 3 stages. Gated: 1 x 4 waves of 64 x 32, BN = 128 (72 KB, two
+//     workgroups per CU); plain: 2 x 4 waves of 32 x 64 (120 KB). At 1024-2048 tokens 12-15% (gate/up)
+//     and 3-7% (down) faster than 1 x 4 waves with 64-byte rows
 //  float8 (128-byte stage rows, one 128-wide MFMA step): bm 64 with BN = 128 and 2 stages (48 KB, three
 //     workgroups per CU); bm 128 in 8-wave workgroups: the plain (down) product 64 x 32 per wave, 2
 //     stages (375 -> 290 us at 4096 tokens), the gated (gate/up) product 64 x 64 per wave with BN = 256
@@ -429,7 +431,10 @@ int launch_dma(GroupArgs& p, int bm, hipStream_t st) {
       if constexpr (ACT == ACT_NONE) return launch_one<T, OutT, ACT, 128, 2, 4, 3, 64, 1, 4>(p, st);
       else return launch_one<T, OutT, ACT, 128, 2, 4, 3, 128, 1, 4>(p, st);
     }
-    if (bm == 64) return launch_one<T, OutT, ACT, 64, 1, 4, 3, 64, 2, 8>(p, st);
+    if (bm == 64) {   // 128-byte stage rows: down in 8 waves, gate/up in two 4-wave workgroups of BN 128
+      if constexpr (ACT == ACT_NONE) return launch_one<T, OutT, ACT, 64, 2, 4, 3, 128, 1, 8>(p, st);
+      else return launch_one<T, OutT, ACT, 64, 1, 4, 3, 128, 2, 8, 128>(p, st);
+    }
   }
   return FLIDE_MOE_ERR_TILE;
 }
