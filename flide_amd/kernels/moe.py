@@ -35,13 +35,13 @@ def tile(pairs: int, fp8: bool, device=None) -> tuple[int, int, int, int, int]:
     Block rows are what `align` pads each expert to. 32 rows (decode) stream each expert's weights through
     LDS in whole 128-byte lines; 16 rows stream them straight into MFMA registers (kept for callers that
     ask for it); 64 and 128 rows are the prefill tiles. The K order is the same for every tile, so the
-    bits do not change with the choice."""
-    if pairs <= 4096:
-        bm = 32
-    elif pairs <= 16384:
-        bm = 64
+    bits do not change with the choice. The switch points are where the two products' summed time
+    crosses on MI355X at the Gemma shape: 16-bit 32 -> 128 rows between 2048 and 3072 pairs (64 rows
+    is never the fastest); float8 32 -> 64 rows past 512 pairs, 64 -> 128 past 8192."""
+    if fp8:
+        bm = 32 if pairs <= 512 else 64 if pairs <= 8192 else 128
     else:
-        bm = 128
+        bm = 32 if pairs <= 2048 else 128
     return bm, BN, 4, 2, 0
 
 

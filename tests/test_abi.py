@@ -159,10 +159,13 @@ def test_tile_choices():
     from flide_amd.kernels import moe
 
     assert moe.tile(512, False)[0] == 32           # decode: weights streamed through LDS in whole lines
-    assert moe.tile(4096, False)[0] == 32
-    assert moe.tile(8192, False)[0] == 64
-    assert moe.tile(16384, False)[0] == 64
-    assert moe.tile(65536, False)[0] == 128        # prefill: LDS-tiled kernels
+    assert moe.tile(2048, False)[0] == 32
+    assert moe.tile(3072, False)[0] == 128         # 16-bit: 128 rows from a few hundred tokens up
+    assert moe.tile(65536, False)[0] == 128
+    assert moe.tile(512, True)[0] == 32            # float8: 64 rows in between
+    assert moe.tile(1024, True)[0] == 64
+    assert moe.tile(8192, True)[0] == 64
+    assert moe.tile(16384, True)[0] == 128
     assert len(moe.tile(65536, True)) == 5
 
 
