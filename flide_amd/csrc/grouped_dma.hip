@@ -125,36 +125,11 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void grouped_dma(Group
   }
   if (pm >= p.nbm || pm * BM >= *p.used) return;
   const long long e = p.blocks[pm];
-  for (int r = tid; r < BM; r += NW * 64) {
-    const int pair = p.rows[pm * BM + r];
-    s_pairs[r] = pair;
-    if constexpr (FP8) {
-      const long long src = p.by_token ? pair / p.topk : pair;
-      s_ascale[r] = pair < p.n_pairs ? p.a_scale[src] : 0.f;
-    }
-  }
-  __syncthreads();
-
   const int K = p.K;
   const int half = p.N / 2;
   const char* A = (const char*)p.a;
   const char* B = (const char*)p.w + e * p.sbe * EB;
-
-  // This lane's global source for each of its loads: tile row (instr * RPI + l / CPR) and logical chunk
-  // c = (l % CPR) ^ swz(row). Instruction rows start at multiples of RPI, so swz(row) and therefore c
-  // (and the chunk's K offset kc) depend on the lane only.
   const int kc = ((l % CPR) ^ swz<CPR>(l / CPR)) * (16 / EB);
-  // Per-lane 32-bit byte offsets from the operands' uniform bases (A rows are gathered pairs, B rows
-  // the expert's weight rows); a stage adds its uniform K offset to the base, so a full stage's load is
-  // base (SGPRs) + offset (one VGPR). Both tensors stay below 4 GB.
-  uint32_t a_off32[LA];
-#pragma unroll
-  for (int i = 0; i < LA; ++i) {
-    const int row = (wave * LA + i) * RPI + l / CPR;
-    const int pair = s_pairs[row];
-    const long long src = pair < p.n_pairs ? (p.by_token ? pair / p.topk : pair) : 0;
-    a_off32[i] = (uint32_t)((src * p.sa + kc) * EB);
-  }
   uint32_t b_off32[LB];
 #pragma unroll
   for (int i = 0; i < LB; ++i) {
@@ -170,7 +145,44 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void grouped_dma(Group
     }
     b_off32[i] = (uint32_t)((n * p.sbn + kc) * EB);
   }
+  // The weight rows' offsets depend only on the expert and the column tile, so the weight parts of the
+  // first NS - 1 stages go in flight before the block's pairs are read (their activation parts follow
+  // in the K loop's prologue, which then waits for both): the workgroup's start-up keeps the memory
+  // pipe busy (the plain product at 8192 tokens 1.5% faster, no change elsewhere).
+  {
+    char* const slots[4] = {lds0, lds1, lds2, lds3};
+#pragma unroll
+    for (int st = 0; st < NS - 1; ++st) {
+      FLIDE_LDS_AS char* sb = (FLIDE_LDS_AS char*)slots[st];
+#pragma unroll
+      for (int i = 0; i < LB; ++i)
+        dma16(B + (long long)st * KS * EB + b_off32[i], sb + A_BYTES + (wave * LB + i) * 1024);
+    }
+  }
+  for (int r = tid; r < BM; r += NW * 64) {
+    const int pair = p.rows[pm * BM + r];
+    s_pairs[r] = pair;
+    if constexpr (FP8) {
+      const long long src = p.by_token ? pair / p.topk : pair;
+      s_ascale[r] = pair < p.n_pairs ? p.a_scale[src] : 0.f;
+    }
+  }
+  __syncthreads();
 
+  // This lane's global source for each of its loads: tile row (instr * RPI + l / CPR) and logical chunk
+  // c = (l % CPR) ^ swz(row). Instruction rows start at multiples of RPI, so swz(row) and therefore c
+  // (and the chunk's K offset kc) depend on the lane only.
+  // Per-lane 32-bit byte offsets from the operands' uniform bases (A rows are gathered pairs, B rows
+  // the expert's weight rows); a stage adds its uniform K offset to the base, so a full stage's load is
+  // base (SGPRs) + offset (one VGPR). Both tensors stay below 4 GB.
+  uint32_t a_off32[LA];
+#pragma unroll
+  for (int i = 0; i < LA; ++i) {
+    const int row = (wave * LA + i) * RPI + l / CPR;
+    const int pair = s_pairs[row];
+    const long long src = pair < p.n_pairs ? (p.by_token ? pair / p.topk : pair) : 0;
+    a_off32[i] = (uint32_t)((src * p.sa + kc) * EB);
+  }
   const int wm = wave % WAVES_M, wn = wave / WAVES_M;
   const int r = l & 15, g = l >> 4;
   // LDS byte offset of this lane's chunk j within a 16-row fragment (16-bit: logical chunk s*4 + g for
@@ -283,9 +295,15 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void grouped_dma(Group
     };
     const int nfull = K / KS;
     // prologue: the host guarantees NS - 1 full stages, so these loads are unconditional (a conditional
-    // load here would again make the wait-count pass conservative at the loop header)
+    // load here would again make the wait-count pass conservative at the loop header); the weight parts
+    // went out first, so the stage counts of wait_stage do not hold until everything has landed
 #pragma unroll
-    for (int st = 0; st < NS - 1; ++st) issue(st, st);
+    for (int st = 0; st < NS - 1; ++st) {   // activation parts; the weight parts are in flight already
+      FLIDE_LDS_AS char* sb = (FLIDE_LDS_AS char*)slot_ptr(st);
+#pragma unroll
+      for (int i = 0; i < LA; ++i) dma16(A + (long long)st * KS * EB + a_off32[i], sb + (wave * LA + i) * 1024);
+    }
+    wait_vmcnt<0>();
     // steady state: stage kt computes while stages kt+1 .. kt+NS-1 load; every stage it issues is full
     const int nmain = nfull - (NS - 1);   // iterations that issue a full stage
     int kt0 = 0;
