@@ -43,6 +43,15 @@ FLIDE_DEV void dma16(const void* src, FLIDE_LDS_AS void* dst) {
   __builtin_amdgcn_global_load_lds((const FLIDE_GLOBAL_AS void*)src, dst, 16, 0, 0);
 }
 
+// The weight loads: non-temporal (`nt`, cache-policy bit 1 on gfx950) when NT, i.e. when every weight
+// byte is read by one workgroup only (decode: an expert's few pairs fill one 32-row block). They then
+// stop displacing the activation rows that the block's column tiles share in L2: at 64 tokens gate/up
+// streams 6.5 TB/s instead of 5.7 (down 6.1 instead of 5.2). Where several blocks share a weight tile
+// (prefill) the same loads are 15-60% slower, so they stay plain there.
+template <bool NT> FLIDE_DEV void dma16w(const void* src, FLIDE_LDS_AS void* dst) {
+  __builtin_amdgcn_global_load_lds((const FLIDE_GLOBAL_AS void*)src, dst, 16, 0, NT ? 2 : 0);
+}
+
 // chunk swizzle of a row with CPR 16-byte chunks (8 for 128-byte rows, 4 for 64-byte rows); both
 // measured bank-conflict-free for the fragment reads below
 template <int CPR> FLIDE_DEV int swz(int row) { return CPR == 8 ? (row & 7) : ((row >> 1) & 3); }
@@ -71,7 +80,7 @@ template <> struct DmaElem<Fp8Tag> {
 };
 
 template <typename T, typename OutT, int ACT, int BM, int BN, int WAVES_M, int WAVES_N, int NS, int ROWB, int OCC,
-          int XCD_CHUNK_BLOCKS>
+          int XCD_CHUNK_BLOCKS, bool NTW>
 __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void grouped_dma(GroupArgs p) {
   constexpr bool FP8 = std::is_same<T, Fp8Tag>::value;
   constexpr int EB = DmaElem<T>::BYTES;
@@ -156,7 +165,7 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void grouped_dma(Group
       FLIDE_LDS_AS char* sb = (FLIDE_LDS_AS char*)slots[st];
 #pragma unroll
       for (int i = 0; i < LB; ++i)
-        dma16(B + (long long)st * KS * EB + b_off32[i], sb + A_BYTES + (wave * LB + i) * 1024);
+        dma16w<NTW>(B + (long long)st * KS * EB + b_off32[i], sb + A_BYTES + (wave * LB + i) * 1024);
     }
   }
   for (int r = tid; r < BM; r += NW * 64) {
@@ -240,7 +249,7 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void grouped_dma(Group
 #pragma unroll
       for (int i = 0; i < LA; ++i) dma16(Ak + a_off32[i], sb + (wave * LA + i) * 1024);
 #pragma unroll
-      for (int i = 0; i < LB; ++i) dma16(Bk + b_off32[i], sb + A_BYTES + (wave * LB + i) * 1024);
+      for (int i = 0; i < LB; ++i) dma16w<NTW>(Bk + b_off32[i], sb + A_BYTES + (wave * LB + i) * 1024);
     };
     // the partial last stage (K % KS != 0): chunks past K read a 16-byte block of zeros
     auto issue_tail = [&](int kt, int slot) {
@@ -253,7 +262,7 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void grouped_dma(Group
         dma16(in ? (const void*)(A + kb + a_off32[i]) : (const void*)g_zero16, sb + (wave * LA + i) * 1024);
 #pragma unroll
       for (int i = 0; i < LB; ++i)
-        dma16(in ? (const void*)(B + kb + b_off32[i]) : (const void*)g_zero16,
+        dma16w<NTW>(in ? (const void*)(B + kb + b_off32[i]) : (const void*)g_zero16,
               sb + A_BYTES + (wave * LB + i) * 1024);
     };
     auto compute = [&](int slot) {
@@ -424,7 +433,7 @@ int launch_one(GroupArgs& p, hipStream_t st) {
   const int items = p.nbm * p.ntn;
   const int round = 8 * p.ntn * XB;
   dim3 grid((items + round - 1) / round * round), block(WM_ * WN_ * 64);
-  grouped_dma<T, OutT, ACT, BM, BN, WM_, WN_, NS, ROWB, OCC, XB><<<grid, block, 0, st>>>(p);
+  grouped_dma<T, OutT, ACT, BM, BN, WM_, WN_, NS, ROWB, OCC, XB, BM == 32><<<grid, block, 0, st>>>(p);
   return FLIDE_MOE_OK;
 }
 
