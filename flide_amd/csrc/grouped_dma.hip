@@ -44,10 +44,10 @@ FLIDE_DEV void dma16(const void* src, FLIDE_LDS_AS void* dst) {
 }
 
 // The weight loads: non-temporal (`nt`, cache-policy bit 1 on gfx950) when NT, i.e. when every weight
-// byte is read by one workgroup only (decode: an expert's few pairs fill one 32-row block). They then
-// stop displacing the activation rows that the block's column tiles share in L2: at 64 tokens gate/up
-// streams 6.5 TB/s instead of 5.7 (down 6.1 instead of 5.2). Where several blocks share a weight tile
-// (prefill) the same loads are 15-60% slower, so they stay plain there.
+// byte is read by one block only (an expert's pairs fill one block). They then stop displacing the
+// activation rows that the block's column tiles share in L2: at 64 tokens gate/up streams 6.5 TB/s
+// instead of 5.7 (down 6.1 instead of 5.2); at 512-1024 tokens the bm-128 gate/up gains 4-6%. Where
+// several blocks share a weight tile (prefill) the same loads are 15-60% slower, so they stay plain.
 template <bool NT> FLIDE_DEV void dma16w(const void* src, FLIDE_LDS_AS void* dst) {
   __builtin_amdgcn_global_load_lds((const FLIDE_GLOBAL_AS void*)src, dst, 16, 0, NT ? 2 : 0);
 }
@@ -433,7 +433,23 @@ int launch_one(GroupArgs& p, hipStream_t st) {
   const int items = p.nbm * p.ntn;
   const int round = 8 * p.ntn * XB;
   dim3 grid((items + round - 1) / round * round), block(WM_ * WN_ * 64);
-  grouped_dma<T, OutT, ACT, BM, BN, WM_, WN_, NS, ROWB, OCC, XB, BM == 32><<<grid, block, 0, st>>>(p);
+  // Non-temporal weight loads (dma16w) for every 32-row (decode) product and for the gated products of
+  // larger tiles while padding fills at least half the blocks (most experts then hold one block, so each
+  // weight tile is read once); the plain (down) products of larger tiles measured slower with them. Only
+  // for weight rows of whole 128-byte lines: a row that ends mid-line (float8 down rows of 704 bytes)
+  // shares that line with the next row, which an `nt` load drops from L2 before it is read again.
+  constexpr int EB = DmaElem<T>::BYTES;
+  const bool lines = (p.sbn * EB) % 128 == 0 && (p.sbe * EB) % 128 == 0 && ((uintptr_t)p.w & 127) == 0;
+  bool nt = false;
+  if constexpr (BM == 32) nt = lines;
+  else if constexpr (ACT != ACT_NONE) nt = lines && 2LL * p.n_pairs <= (long long)p.nbm * BM;
+  if constexpr (BM == 32 || ACT != ACT_NONE) {
+    if (nt) {
+      grouped_dma<T, OutT, ACT, BM, BN, WM_, WN_, NS, ROWB, OCC, XB, true><<<grid, block, 0, st>>>(p);
+      return FLIDE_MOE_OK;
+    }
+  }
+  grouped_dma<T, OutT, ACT, BM, BN, WM_, WN_, NS, ROWB, OCC, XB, false><<<grid, block, 0, st>>>(p);
   return FLIDE_MOE_OK;
 }
 
