@@ -159,12 +159,17 @@ __global__ __launch_bounds__(RW_THREADS) void combine_norm_bf16_kernel(const YT*
     for (int j = 0; j < KMAX; ++j) {
       if (j >= k) break;
       const long long row = (t * k + j) * (long long)H;
+      // y is read exactly once: non-temporal loads keep it from evicting what the other wavefronts'
+      // rows still need (combine_norm at 8192 tokens: 153 -> 134 us, 6.2 TB/s)
       if constexpr (std::is_same<YT, float>::value) {
-        yv[j] = ((const float4*)(y + row))[c4];
+        typedef float f32x4v __attribute__((ext_vector_type(4)));
+        const f32x4v t = __builtin_nontemporal_load((const f32x4v*)(y + row) + c4);
+        yv[j] = make_float4(t[0], t[1], t[2], t[3]);
       } else {
-        const uint2 raw = ((const uint2*)(y + row))[c4];
-        yv[j] = make_float4(bf16_to_f32(raw.x & 0xffff), bf16_to_f32(raw.x >> 16), bf16_to_f32(raw.y & 0xffff),
-                            bf16_to_f32(raw.y >> 16));
+        typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+        const u32x2v raw = __builtin_nontemporal_load((const u32x2v*)(y + row) + c4);
+        yv[j] = make_float4(bf16_to_f32(raw[0] & 0xffff), bf16_to_f32(raw[0] >> 16), bf16_to_f32(raw[1] & 0xffff),
+                            bf16_to_f32(raw[1] >> 16));
       }
     }
 #pragma unroll
