@@ -1,7 +1,8 @@
 """Timing of the steps on either side of the MoE layer at the Gemma 4 shape (H 2816, E 128, top-8, bf16):
 in front, the router, rms_norm, the reference's three-call glue (rms_norm -> router, rms_norm;
 flide/backbones/gemma4/fused.py:234-237) and the fused router_norm, with torch.mm (hipBLASLt) beside the router
-for scale; behind, combine_norm alone and fused with the post-norm step (combine_norm_sandwich, fused.py:215,224).
+for scale; behind, combine_norm alone and fused with the post-norm step (combine_norm_sandwich, fused.py:215,224),
+and Qwen's combine (moe.py:256-277) at the same shape.
 
 Each entry is the mean over 20 replays of a HIP graph holding 20 calls, so one launch of a small kernel
 (about 4-5 us) is part of every figure, as it is inside a captured layer. Prints one JSON line per batch size.
@@ -65,6 +66,7 @@ def run(tokens) -> list[dict]:
         dense = torch.randn(T, H, device=dev, generator=gen).to(torch.bfloat16)
         w1, w2, wp, wn = (torch.rand(H, device=dev, generator=gen).to(torch.bfloat16) + 0.5 for _ in range(4))
         sc = torch.tensor([0.75], device=dev, dtype=torch.bfloat16)
+        gl = torch.randn(T, 1, device=dev, generator=gen)
 
         row = {"tokens": T, "unit": "us per call",
                "router": _graph_us(lambda: moe.router(r, wr)),
@@ -74,7 +76,8 @@ def run(tokens) -> list[dict]:
                "router_norm": _graph_us(lambda: moe.router_norm(h, nw, wr, EPS, n2)),
                "combine_norm": _graph_us(lambda: moe.combine_norm(y, dense, w1, w2, 8, EPS)),
                "combine_norm_sandwich": _graph_us(
-                   lambda: moe.combine_norm_sandwich(y, dense, w1, w2, 8, EPS, h, wp, sc, wn))}
+                   lambda: moe.combine_norm_sandwich(y, dense, w1, w2, 8, EPS, h, wp, sc, wn)),
+               "combine_qwen": _graph_us(lambda: moe.combine(y, dense, gl, 8))}
         del y
         row = {k: (round(v, 2) if isinstance(v, float) else v) for k, v in row.items()}
         print(json.dumps(row), flush=True)

@@ -255,6 +255,54 @@ __global__ __launch_bounds__(RW_THREADS) void combine_norm_bf16_kernel(const YT*
   }
 }
 
+// combine (Qwen), vectorised for y float32 or bf16 with bf16 shared and out, H % 4 == 0, H <= 4096 and
+// k <= 8: one workgroup per token, the k rows summed in slot order in registers, y read non-temporally
+// (each element is read once), then + shared * sigmoid(gate) and one rounding (moe.py:256-277).
+template <typename YT>
+__global__ __launch_bounds__(RW_THREADS) void combine_vec_kernel(const YT* __restrict__ y,
+                                                                 const u16* __restrict__ shared,
+                                                                 const float* __restrict__ gate,
+                                                                 u16* __restrict__ out, int H, int k) {
+  constexpr int V = 4, KMAX = 8;
+  const long long t = blockIdx.x;
+  const int nv = H / 4;
+  const float sg = 1.0f / (1.0f + expf(-gate[t]));
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    const int c4 = threadIdx.x + v * RW_THREADS;
+    if (c4 >= nv) continue;
+    float4 yv[KMAX];
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j) {
+      if (j >= k) break;
+      const long long row = (t * k + j) * (long long)H;
+      if constexpr (std::is_same<YT, float>::value) {
+        typedef float f32x4v __attribute__((ext_vector_type(4)));
+        const f32x4v q = __builtin_nontemporal_load((const f32x4v*)(y + row) + c4);
+        yv[j] = make_float4(q[0], q[1], q[2], q[3]);
+      } else {
+        typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+        const u32x2v raw = __builtin_nontemporal_load((const u32x2v*)(y + row) + c4);
+        yv[j] = make_float4(bf16_to_f32(raw[0] & 0xffff), bf16_to_f32(raw[0] >> 16), bf16_to_f32(raw[1] & 0xffff),
+                            bf16_to_f32(raw[1] >> 16));
+      }
+    }
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j) {   // slot order
+      if (j >= k) break;
+      acc.x += yv[j].x; acc.y += yv[j].y; acc.z += yv[j].z; acc.w += yv[j].w;
+    }
+    const uint2 sr = ((const uint2*)(shared + t * H))[c4];
+    uint2 o;
+    o.x = (uint32_t)f32_to_bf16(acc.x + bf16_to_f32(sr.x & 0xffff) * sg) |
+          ((uint32_t)f32_to_bf16(acc.y + bf16_to_f32(sr.x >> 16) * sg) << 16);
+    o.y = (uint32_t)f32_to_bf16(acc.z + bf16_to_f32(sr.y & 0xffff) * sg) |
+          ((uint32_t)f32_to_bf16(acc.w + bf16_to_f32(sr.y >> 16) * sg) << 16);
+    ((uint2*)(out + t * H))[c4] = o;
+  }
+}
+
 // combine (Qwen): sum of the k rows + shared * sigmoid(gate); one workgroup per (token, 1024 columns)
 template <int YDT>
 __global__ __launch_bounds__(RW_THREADS) void combine_kernel(const void* __restrict__ y,
@@ -439,6 +487,15 @@ extern "C" int flide_moe_combine(const void* y, int y_dtype, const void* shared,
     return FLIDE_MOE_ERR_ARG;
   if (T == 0) return FLIDE_MOE_OK;
   hipStream_t st = (hipStream_t)stream;
+  if (out_dtype == FLIDE_BF16 && (y_dtype == FLIDE_F32 || y_dtype == FLIDE_BF16) && H % 4 == 0 &&
+      H <= 4 * 4 * RW_THREADS && k <= 8 && !((uintptr_t)y & 15) && !(((uintptr_t)shared | (uintptr_t)out) & 7)) {
+    if (y_dtype == FLIDE_F32)
+      combine_vec_kernel<float><<<T, RW_THREADS, 0, st>>>((const float*)y, (const u16*)shared, gate, (u16*)out, H, k);
+    else
+      combine_vec_kernel<u16><<<T, RW_THREADS, 0, st>>>((const u16*)y, (const u16*)shared, gate, (u16*)out, H, k);
+    FLIDE_CHECK_LAUNCH();
+    return FLIDE_MOE_OK;
+  }
   dim3 grid(T, (H + 1023) / 1024);
   if (y_dtype == FLIDE_F32)
     combine_kernel<FLIDE_F32><<<grid, RW_THREADS, 0, st>>>(y, shared, gate, out, out_dtype, H, k);

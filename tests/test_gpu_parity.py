@@ -300,16 +300,19 @@ def test_combine_norm_sandwich(ydt, scale, nxt):
         np.testing.assert_allclose(np32(x_out), gx, rtol=2 ** -6, atol=1e-6)
 
 
-def test_combine_qwen():
-    print("combine", flush=True)
+@pytest.mark.parametrize("ydt,H,k", [(torch.float32, 2048 + 64, 4), (torch.bfloat16, 2048, 8),
+                                     (torch.float32, 4100, 3), (torch.float32, 2048, 10)])
+def test_combine_qwen(ydt, H, k):
+    """The vector kernel (f32 and bf16 y), and the scalar one for H past 4096 or k past 8."""
+    print(f"combine y {ydt} H={H} k={k}", flush=True)
     moe = _moe()
     g = torch.Generator().manual_seed(12)
-    T, H, k = 19, 2048 + 64, 4
-    y = torch.randn(T * k, H, generator=g)
+    T = 19
+    y = torch.randn(T * k, H, generator=g).to(ydt)
     shared = torch.randn(T, H, generator=g).to(torch.bfloat16)
     gate = torch.randn(T, 1, generator=g)
     out = moe.combine(y.to(DEV), shared.to(DEV), gate.to(DEV), k)
-    ref = orc.combine(y.numpy(), np32(shared), gate.numpy(), k)
+    ref = orc.combine(np32(y), np32(shared), gate.numpy(), k)
     np.testing.assert_allclose(np32(out), ref, rtol=2 ** -7, atol=1e-6)
 
 
