@@ -336,6 +336,35 @@ def test_quantize_rows_bit_exact(dt, K):
     np.testing.assert_array_equal(q.cpu().view(torch.uint8).numpy(), orc.e4m3fn_encode(rq))
 
 
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("K", [704, 2816])
+def test_quantize_rows_vec_matches_division(dt, K):
+    """The 16-bit kernel's quotient (x * (1/s) and one fma correction) against the float32 kernel's true
+    division on the same values, byte for byte: rows of 16-bit bit patterns drawn uniformly below a random
+    amax (log-uniform magnitudes, so exact e4m3 ties, subnormals and values under the smallest code are
+    common), and rows holding +-inf or NaN (an inf scale takes the division in both kernels)."""
+    print(f"quantize vec vs division {dt} K={K}", flush=True)
+    from flide_amd.kernels import fp8
+
+    g = np.random.default_rng(21)
+    M = 256
+    finite_max = 0x7F7F if dt == torch.bfloat16 else 0x7BFF
+    amax_bits = g.integers(1, finite_max, M)
+    bits = (g.random((M, K)) * amax_bits[:, None]).astype(np.int64)
+    bits[:, 0] = amax_bits
+    bits |= np.where(g.random((M, K)) < 0.5, 0x8000, 0)   # sign
+    x = torch.from_numpy(bits.astype(np.uint16).view(np.int16)).view(dt)
+    inf, nan = float("inf"), float("nan")
+    x[0, :4] = torch.tensor([inf, 1.0, -0.0, -3.0])
+    x[1, 5], x[2, 7], x[3, 9] = -inf, nan, nan
+    x[4] = 0.0
+    x[4, 3] = -0.0
+    q, s = fp8.quantize_tokens(x.to(DEV))
+    qf, sf = fp8.quantize_tokens(x.float().to(DEV))
+    np.testing.assert_array_equal(s.cpu().numpy(), sf.cpu().numpy())
+    np.testing.assert_array_equal(q.cpu().view(torch.uint8).numpy(), qf.cpu().view(torch.uint8).numpy())
+
+
 def test_quantize_experts_matches_rows():
     print("quantize_experts", flush=True)
     moe = _moe()
