@@ -399,6 +399,232 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void grouped_dma(Group
   }
 }
 
+// Float8 plain (down) products with short rows (K <= 768, the 704-wide down product): the block's
+// activation rows stay resident in LDS and one loader wave streams the expert's weight tiles through a
+// ring, continuously over several column tiles. With K this short, the per-tile kernel above spends
+// most of a block's life filling and draining its ring (6 stages per tile); here the ring runs across
+// tile boundaries and the activation rows are read once per block, not once per tile.
+//
+// Roles: waves 0-7 (2 x 4, each 64 rows x 32 columns of a 128 x 128 tile) load the activation rows
+// once, then only read LDS, issue MFMAs and store; wave 8 only issues direct-to-LDS weight loads and
+// waits for them. A wave's vmcnt counts its own memory operations, so the compute waves' epilogue
+// stores never hold up the loads' waits (in a single-role kernel every wait after a store would wait
+// for that store too). One barrier per stage: at stage s the loader has waited for stage s and the
+// compute waves have finished stage s - 1, whose ring slot the loader refills right after it.
+// The column scales of tile t travel with every stage of tile t (BN / 64 loads of 256 bytes, so every
+// stage holds the same number of loads) into s_ws[t & 1], read by the tile's epilogue.
+//
+// Arithmetic: the same 128-wide K steps, lane mapping, MFMA and epilogue order as grouped_dma, so the
+// output bits are the same.
+template <typename OutT, int NS, int BN, int KT_MAX, int XB>
+__global__ __launch_bounds__(9 * 64, 1) void grouped_fp8_resident(GroupArgs p, int tpb, int nch) {
+  constexpr int BM = 128, ROWB = 128;
+  constexpr int WAVES_M = 2, WM = 64, WN = BN / 4, FM = 4, FN = WN / 16;
+  constexpr int A_KT = BM * ROWB, B_BYTES = BN * ROWB;
+  constexpr int LB = BN / 8, LW = BN / 64, LPS = LB + LW;   // loads per stage: weight rows, scales
+  static_assert((NS - 1) * LPS < 64 && 2 * KT_MAX < 64, "loads in flight must fit vmcnt");
+  static_assert(NS >= 3 && NS <= 6 && BN % 64 == 0 && FN >= 1, "ring of 3..6 slots, 64-row multiples");
+
+  __shared__ __attribute__((aligned(1024))) char s_a[KT_MAX * A_KT];
+  __shared__ __attribute__((aligned(1024))) char s_b[NS * B_BYTES];
+  __shared__ __attribute__((aligned(16))) float s_ws[2][BN];
+  __shared__ int s_pairs[BM];
+  __shared__ float s_ascale[BM];
+  __shared__ float s_wt[BM];
+
+  const int tid = threadIdx.x, l = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // items (block, column chunk), chunked per XCD as in grouped_dma
+  const int CH = nch * XB;
+  const int b = blockIdx.x;
+  const int j = b >> 3;
+  const int widx = ((j / CH) * 8 + (b & 7)) * CH + j % CH;
+  const int pm = widx / nch, c = widx % nch;
+  if (pm >= p.nbm || pm * BM >= *p.used) return;
+  const int ntn = (p.N + BN - 1) / BN;
+  const int t0 = c * tpb, nt = min(t0 + tpb, ntn) - t0;
+  if (nt <= 0) return;
+  const int K = p.K, KT = (K + ROWB - 1) / ROWB;
+  const int S = nt * KT;
+  const long long e = p.blocks[pm];
+  for (int r = tid; r < BM; r += 9 * 64) {
+    const int pair = p.rows[pm * BM + r];
+    s_pairs[r] = pair;
+    const bool ok = pair < p.n_pairs;
+    const long long src = p.by_token ? pair / p.topk : pair;
+    s_ascale[r] = ok ? p.a_scale[src] : 0.f;
+    s_wt[r] = ok && p.weights ? p.weights[pair] : 1.f;
+  }
+  __syncthreads();
+  // lane l of a 1 KB load fills row l / 8 (of 8) at chunk position l % 8, which holds logical chunk
+  // (l % 8) ^ (row & 7); rows start at multiples of 8, so the chunk's byte offset depends on l only
+  const int kc = ((l & 7) ^ (l >> 3)) * 16;
+
+  if (wave == 8) {   // ---------------- loader ----------------
+    const char* B = (const char*)p.w + e * p.sbe;
+    const float* WS = p.w_scale + e * p.sse;
+    auto issue = [&](int s) {
+      const int t = t0 + s / KT, kt = s % KT, slot = s % NS;
+      FLIDE_LDS_AS char* sb = (FLIDE_LDS_AS char*)(s_b + slot * B_BYTES);
+      const int k0 = kt * ROWB;
+      const bool in = k0 + kc < K;
+#pragma unroll
+      for (int i = 0; i < LB; ++i) {
+        const int n = min(t * BN + i * 8 + (l >> 3), p.N - 1);
+        dma16(in ? (const void*)(B + (long long)n * p.sbn + k0 + kc) : (const void*)g_zero16, sb + i * 1024);
+      }
+#pragma unroll
+      for (int i = 0; i < LW; ++i) {
+        const int col = min(t * BN + i * 64 + l, p.N - 1);
+        __builtin_amdgcn_global_load_lds((const FLIDE_GLOBAL_AS void*)(WS + col),
+                                         (FLIDE_LDS_AS void*)&s_ws[t & 1][i * 64], 4, 0, 0);
+      }
+    };
+    for (int s = 0; s < NS - 1 && s < S; ++s) issue(s);
+    for (int s = 0; s < S; ++s) {
+      const int ahead = min(NS - 2, S - 1 - s);   // stages after s already in flight
+      if (NS > 5 && ahead >= 4) wait_vmcnt<(NS > 5 ? 4 : 0) * LPS>();
+      else if (NS > 4 && ahead >= 3) wait_vmcnt<(NS > 4 ? 3 : 0) * LPS>();
+      else if (NS > 3 && ahead >= 2) wait_vmcnt<(NS > 3 ? 2 : 0) * LPS>();
+      else if (ahead >= 1) wait_vmcnt<LPS>();
+      else wait_vmcnt<0>();
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      if (s + NS - 1 < S) issue(s + NS - 1);
+    }
+    return;
+  }
+
+  // ---------------- compute waves ----------------
+  {
+    const char* A = (const char*)p.a;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int row = (wave * 2 + q) * 8 + (l >> 3);
+      const int pair = s_pairs[row];
+      const long long src = pair < p.n_pairs ? (p.by_token ? pair / p.topk : pair) : 0;
+      const char* ar = A + src * p.sa;
+      for (int kt = 0; kt < KT; ++kt) {
+        const bool in = kt * ROWB + kc < K;
+        dma16(in ? (const void*)(ar + kt * ROWB + kc) : (const void*)g_zero16,
+              (FLIDE_LDS_AS char*)(s_a + kt * A_KT) + (wave * 2 + q) * 1024);
+      }
+    }
+    wait_vmcnt<0>();
+  }
+  const int wm = wave % WAVES_M, wn = wave / WAVES_M;
+  const int r = l & 15, g = l >> 4;
+  int lane_off[2];
+#pragma unroll
+  for (int jj = 0; jj < 2; ++jj) lane_off[jj] = r * ROWB + ((((jj * 4 + g) % 8) ^ (r & 7)) << 4);
+  int nlive = 0;
+#pragma unroll
+  for (int fm = 0; fm < FM; ++fm)
+    nlive += __builtin_amdgcn_readfirstlane(s_pairs[wm * WM + fm * 16]) < p.n_pairs ? 1 : 0;
+  typedef typename OutTraits<OutT>::storage St;
+
+  auto run = [&](auto fma_tag) {
+    constexpr int FMA = decltype(fma_tag)::value;
+    f32x4_t acc[FM][FN];
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn) acc[fm][fn] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    // the wave's rows are the same for every tile: their pair, activation scale and routing weight
+    // stay in registers (row wm * WM + fm * 16 + g * 4 + i of output register i)
+    constexpr int FR = FMA > 0 ? FMA : 1;
+    int prow[FR][4];
+    float rsc[FR][4], rwt[FR][4];
+#pragma unroll
+    for (int fm = 0; fm < FR; ++fm)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = wm * WM + fm * 16 + g * 4 + i;
+        prow[fm][i] = s_pairs[row];
+        rsc[fm][i] = s_ascale[row];
+        rwt[fm][i] = s_wt[row];
+      }
+    const bool mulw = p.weights != nullptr;
+    int kt = 0, slot = 0, t = t0;
+    for (int s = 0; s < S; ++s) {
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      if constexpr (FMA > 0) {
+        const char* sa_ = s_a + kt * A_KT + wm * WM * ROWB;
+        const char* sb_ = s_b + slot * B_BYTES + wn * WN * ROWB;
+        i32x8_t af[FMA], bfr[FN];
+#pragma unroll
+        for (int fm = 0; fm < FMA; ++fm) {
+          const u32x4_t lo = *(const u32x4_t*)(sa_ + fm * 16 * ROWB + lane_off[0]);
+          const u32x4_t hi = *(const u32x4_t*)(sa_ + fm * 16 * ROWB + lane_off[1]);
+          af[fm] = i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+        }
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn) {
+          const u32x4_t lo = *(const u32x4_t*)(sb_ + fn * 16 * ROWB + lane_off[0]);
+          const u32x4_t hi = *(const u32x4_t*)(sb_ + fn * 16 * ROWB + lane_off[1]);
+          bfr[fn] = i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+        }
+#pragma unroll
+        for (int fm = 0; fm < FMA; ++fm)
+#pragma unroll
+          for (int fn = 0; fn < FN; ++fn) acc[fm][fn] = mfma_fp8(af[fm], bfr[fn], acc[fm][fn]);
+        if (kt == KT - 1) {   // epilogue of tile t: out = acc * s_a[row] * s_w[col] (* routing weight)
+          float cs[FN];
+#pragma unroll
+          for (int fn = 0; fn < FN; ++fn) cs[fn] = s_ws[t & 1][wn * WN + fn * 16 + r];
+#pragma unroll
+          for (int fm = 0; fm < FMA; ++fm) {
+#pragma unroll
+            for (int fn = 0; fn < FN; ++fn) {
+              const int col = t * BN + wn * WN + fn * 16 + r;
+#pragma unroll
+              for (int i = 0; i < 4; ++i) {
+                const int pair = prow[fm][i];
+                if (pair < p.n_pairs && col < p.N) {
+                  float v = acc[fm][fn][i] * rsc[fm][i] * cs[fn];
+                  if (mulw) v *= rwt[fm][i];
+                  ((St*)p.out)[(long long)pair * p.sc + col] = OutTraits<OutT>::conv(v);
+                }
+              }
+              acc[fm][fn] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+            }
+          }
+        }
+      }
+      if (++slot == NS) slot = 0;
+      if (++kt == KT) { kt = 0; ++t; }
+    }
+  };
+  if (nlive == 0) run(std::integral_constant<int, 0>{});
+  else if (nlive == 1) run(std::integral_constant<int, 1>{});
+  else if (nlive == 2) run(std::integral_constant<int, 2>{});
+  else if (nlive == 3) run(std::integral_constant<int, 3>{});
+  else run(std::integral_constant<int, 4>{});
+}
+
+// grouped_fp8_resident for a float8 plain product with 128-row blocks: K of 129..768 (whole 16-byte
+// chunks). Column tiles are split into chunks so that the grid holds at least about 640 items
+// (2.5 per CU at one workgroup per CU); returns FLIDE_MOE_ERR_TILE when the shape does not fit.
+template <typename OutT, int NS = 3, int BN = 128>
+int launch_fp8_resident(GroupArgs& p, hipStream_t st) {
+  constexpr int KT_MAX = 6, XB = 4;
+  // s_ws[t & 1] is refilled for tile t + 2 from stage (t + 2) * KT - (NS - 1) on, which must come after
+  // tile t's epilogue (stage (t + 1) * KT - 1): KT >= NS - 1 stages of K
+  if (p.K <= (NS - 2) * 128 || p.K > KT_MAX * 128 || p.K % 16) return FLIDE_MOE_ERR_TILE;
+  const int ntn = (p.N + BN - 1) / BN;
+  int nch = (640 + p.nbm - 1) / max(p.nbm, 1);
+  nch = max(1, min(nch, ntn));
+  const int tpb = (ntn + nch - 1) / nch;
+  nch = (ntn + tpb - 1) / tpb;
+  p.ntn = ntn;
+  const int items = p.nbm * nch;
+  const int round = 8 * nch * XB;
+  dim3 grid((items + round - 1) / round * round), block(9 * 64);
+  grouped_fp8_resident<OutT, NS, BN, KT_MAX, XB><<<grid, block, 0, st>>>(p, tpb, nch);
+  return FLIDE_MOE_OK;
+}
+
 // Tiles (default BN = 256 weight rows). Two waves per SIMD matter more than deeper rings or larger
 // tiles here (measured: variants with one wave per SIMD lose 15-40% on gfx950; rings of 4-6 stages
 // were slower too): either two 4-wave workgroups per CU, or one 8-wave workgroup:
@@ -460,7 +686,10 @@ int launch_dma(GroupArgs& p, int bm, hipStream_t st) {
     if (bm == 32) return launch_one<T, OutT, ACT, 32, 1, 4, 3, 128, 2, 8, 128>(p, st);
     if (bm == 256) return launch_one<T, OutT, ACT, 256, 1, 4, 2, 128, 1, 2>(p, st);
     if (bm == 128) {   // 8 waves: down 64 x 32 each (BN 128), gate/up 64 x 64 each (BN 256, 3 stages)
-      if constexpr (ACT == ACT_NONE) return launch_one<T, OutT, ACT, 128, 2, 4, 2, 128, 2, 4, 128>(p, st);
+      if constexpr (ACT == ACT_NONE) {
+        if (launch_fp8_resident<OutT>(p, st) == FLIDE_MOE_OK) return FLIDE_MOE_OK;
+        return launch_one<T, OutT, ACT, 128, 2, 4, 2, 128, 2, 4, 128>(p, st);
+      }
       else return launch_one<T, OutT, ACT, 128, 2, 4, 3, 128, 1, 4, 256>(p, st);
     }
     if (bm == 64) return launch_one<T, OutT, ACT, 64, 1, 4, 2, 128, 2, 8, 128>(p, st);
