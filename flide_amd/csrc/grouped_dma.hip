@@ -638,7 +638,7 @@ int launch_fp8_resident(GroupArgs& p, hipStream_t st) {
 //     and 3-7% (down) faster than 1 x 4 waves with 64-byte rows
 //  float8 (128-byte stage rows, one 128-wide MFMA step): bm 64 with BN = 128 and 2 stages (48 KB, three
 //     workgroups per CU); bm 128 in 8-wave workgroups: the plain (down) product 64 x 32 per wave, 2
-//     stages (375 -> 290 us at 4096 tokens), the gated (gate/up) product 64 x 64 per wave with BN = 256
+//     stages (375 -> 290 us at 4096 tokens; with K <= 768 grouped_fp8_resident replaces it, 251 us), the gated (gate/up) product 64 x 64 per wave with BN = 256
 //     and 3 stages (144 KB; 5-10% faster than 2 x 2 waves of BN 128 at 4096-16384 tokens); bm 256:
 //     2 stages = 128 KB
 //  bm 32 (decode): 128-byte stage rows, 3 stages. 16-bit: BN = 64 (gated 2 x 2 waves, plain 1 x 4),
@@ -685,7 +685,7 @@ int launch_dma(GroupArgs& p, int bm, hipStream_t st) {
   if constexpr (FP8) {
     if (bm == 32) return launch_one<T, OutT, ACT, 32, 1, 4, 3, 128, 2, 8, 128>(p, st);
     if (bm == 256) return launch_one<T, OutT, ACT, 256, 1, 4, 2, 128, 1, 2>(p, st);
-    if (bm == 128) {   // 8 waves: down 64 x 32 each (BN 128), gate/up 64 x 64 each (BN 256, 3 stages)
+    if (bm == 128) {   // 8 waves: down 64 x 32 each (BN 128; K <= 768: grouped_fp8_resident), gate/up 64 x 64 each (BN 256, 3 stages)
       if constexpr (ACT == ACT_NONE) {
         if (launch_fp8_resident<OutT>(p, st) == FLIDE_MOE_OK) return FLIDE_MOE_OK;
         return launch_one<T, OutT, ACT, 128, 2, 4, 2, 128, 2, 4, 128>(p, st);
