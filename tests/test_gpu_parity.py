@@ -198,6 +198,38 @@ def test_grouped_short_k(bm, fp8, K):
     assert_close(np32(out), ref, REL_BF16, f"short K bm={bm}")
 
 
+@pytest.mark.parametrize("T,E,k,N,K,odt,mul_w,by_token", [
+    (1200, 128, 8, 2816, 704, torch.bfloat16, True, False),    # the Gemma down product
+    (1100, 16, 4, 2000, 208, torch.float32, False, False),     # K and N tails
+    (700, 8, 2, 333, 768, torch.float16, True, True),          # longest K, rows by token
+    (2048, 64, 8, 512, 144, torch.bfloat16, False, True),
+])
+def test_grouped_fp8_plain_bm128(T, E, k, N, K, odt, mul_w, by_token):
+    """The FP8 plain product at bm 128 with K <= 768 (activation rows resident in LDS, weight tiles
+    streamed across column tiles) against the dequantised computation."""
+    print(f"grouped fp8 plain bm128 T={T} N={N} K={K} {odt}", flush=True)
+    moe = _moe()
+    g = torch.Generator().manual_seed(T + K)
+    _, ids = orc.route(torch.randn(T, E, generator=g).numpy(), k)
+    x = torch.randn(T if by_token else T * k, K, generator=g).to(torch.bfloat16)
+    w = (torch.randn(E, N, K, generator=g) * 0.05).to(torch.bfloat16)
+    wts = torch.rand(T * k, generator=g)
+    rows, blocks, used = moe.align(torch.from_numpy(ids).to(DEV), E, 128)
+    out = torch.full((T * k, N), float("nan"), device=DEV, dtype=odt)
+    qw, sw = orc.quantize_experts(np32(w))
+    qx, sx = orc.quantize_tokens(np32(x))
+    wq = torch.from_numpy(orc.e4m3fn_encode(qw)).view(torch.float8_e4m3fn).to(DEV)
+    moe.grouped_fp8(x.to(DEV), wq, torch.from_numpy(sw).to(DEV), out, rows, blocks, used, k, by_token,
+                    wts.to(DEV) if mul_w else None, tile=(128, 128, 4, 2))
+    al = orc.align(ids, E, 128)
+    odn = {torch.bfloat16: "bf16", torch.float16: "f16", torch.float32: "fp32"}[odt]
+    ref = orc.grouped(qx * sx, qw * sw[:, :, None], al["rows"], al["blocks"], al["used"], T * k, k, by_token,
+                      wts.numpy() if mul_w else None, bm=128, out_dtype=odn)
+    assert not np.isnan(np32(out)).any(), "a valid pair's row was not written"
+    # float32 out: fp32 accumulation against the oracle's float64 (the FP8 bar is 3e-2)
+    assert_close(np32(out), ref, REL_BF16 if odt != torch.float32 else 1e-4, "fp8 plain bm128")
+
+
 def _experts_case(cfg, T=None, pairs_subset=None, fp8=False):
     moe = _moe()
     d = inputs(cfg, 0, T)
