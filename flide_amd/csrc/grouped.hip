@@ -23,13 +23,9 @@
 
 #include "grouped_common.hpp"
 
-// weight loads of the streaming kernels: ordinary loads measured faster than non-temporal ones on
-// MI355X for this pattern (5.6 vs 4.75 TB/s at the decode shape)
-#ifdef FLIDE_STREAM_NT_LOADS
-#define FLIDE_WLOAD(p) __builtin_nontemporal_load(p)
-#else
+// weight loads of the streaming kernels are ordinary loads: they measured faster than non-temporal
+// ones on MI355X for this pattern (5.6 vs 4.75 TB/s at the decode shape)
 #define FLIDE_WLOAD(p) (*(p))
-#endif
 
 namespace {
 using namespace grouped_detail;
@@ -603,34 +599,15 @@ __global__ __launch_bounds__(256) void grouped_stream8(GroupArgs p) {
 // ---------------------------------------------------------------------------------------------------
 // Compiled tiles: bm 32/64/128/256 -> direct-to-LDS kernels (grouped_dma.hip); bm 16, and bm 32 when K is
 // too short for their ring -> stream kernels (4 waves x NF fragments); bm 64/128/256 with K too short
-// for the ring (or under FLIDE_MOE_LEGACY_LDS=1) -> the register-staged LDS kernels below.
-#ifndef FLIDE_STREAM_NF
-#define FLIDE_STREAM_NF 2
-#endif
-#ifndef FLIDE_STREAM_U
-#define FLIDE_STREAM_U 4
-#endif
-#ifndef FLIDE_STREAM_NF_DOWN
-#define FLIDE_STREAM_NF_DOWN 2
-#endif
-constexpr int STREAM_NF = FLIDE_STREAM_NF;  // 16-row weight fragments per wave (gated products)
-constexpr int STREAM_NF_DOWN = FLIDE_STREAM_NF_DOWN;  // ... and for the plain (down) products
-
-// FLIDE_MOE_LEGACY_LDS=1 selects the register-staged LDS kernels instead of the direct-to-LDS ones
-// for 64/128-row tiles (same arithmetic and bits; kept for comparison).
-bool legacy_lds() {
-  static const bool v = [] {
-    const char* s = getenv("FLIDE_MOE_LEGACY_LDS");
-    return s && s[0] == '1';
-  }();
-  return v;
-}
-constexpr int STREAM_U = FLIDE_STREAM_U;   // K chunks in flight per wave
+// for the ring -> the register-staged LDS kernels above.
+constexpr int STREAM_NF = 2;       // 16-row weight fragments per wave (gated products)
+constexpr int STREAM_NF_DOWN = 2;  // ... and for the plain (down) products
+constexpr int STREAM_U = 4;        // K chunks in flight per wave
 
 template <typename T, typename OutT, int ACT>
 int launch16(GroupArgs& p, int bm, hipStream_t st) {
   dim3 block(256);
-  if (bm == 32 && !legacy_lds()) {   // the direct-to-LDS kernel streams whole lines (grouped_dma.hip)
+  if (bm == 32) {   // the direct-to-LDS kernel streams whole lines (grouped_dma.hip)
     const int out_dtype = std::is_same<OutT, float>::value ? FLIDE_F32
                           : std::is_same<OutT, Bf16Out>::value ? FLIDE_BF16 : FLIDE_F16;
     const int rc = dma_dispatch16(p, std::is_same<T, __bf16>::value, out_dtype, ACT, bm, st);
@@ -647,7 +624,7 @@ int launch16(GroupArgs& p, int bm, hipStream_t st) {
     else grouped_stream16<T, OutT, ACT, 2, NF, STREAM_U><<<grid, block, 0, st>>>(p);
     return FLIDE_MOE_OK;
   }
-  if ((bm == 64 || bm == 128 || bm == 256) && !legacy_lds()) {
+  if (bm == 64 || bm == 128 || bm == 256) {
     const int out_dtype = std::is_same<OutT, float>::value ? FLIDE_F32
                           : std::is_same<OutT, Bf16Out>::value ? FLIDE_BF16 : FLIDE_F16;
     const int rc = dma_dispatch16(p, std::is_same<T, __bf16>::value, out_dtype, ACT, bm, st);
@@ -670,7 +647,7 @@ int launch16(GroupArgs& p, int bm, hipStream_t st) {
 template <typename OutT, int ACT>
 int launch8(GroupArgs& p, int bm, hipStream_t st) {
   dim3 block(256);
-  if (bm == 32 && !legacy_lds()) {
+  if (bm == 32) {
     const int out_dtype = std::is_same<OutT, float>::value ? FLIDE_F32
                           : std::is_same<OutT, Bf16Out>::value ? FLIDE_BF16 : FLIDE_F16;
     const int rc = dma_dispatch8(p, out_dtype, ACT, bm, st);
@@ -687,7 +664,7 @@ int launch8(GroupArgs& p, int bm, hipStream_t st) {
     else grouped_stream8<OutT, ACT, 2, NF, STREAM_U><<<grid, block, 0, st>>>(p);
     return FLIDE_MOE_OK;
   }
-  if ((bm == 64 || bm == 128 || bm == 256) && !legacy_lds()) {
+  if (bm == 64 || bm == 128 || bm == 256) {
     const int out_dtype = std::is_same<OutT, float>::value ? FLIDE_F32
                           : std::is_same<OutT, Bf16Out>::value ? FLIDE_BF16 : FLIDE_F16;
     const int rc = dma_dispatch8(p, out_dtype, ACT, bm, st);
@@ -741,6 +718,14 @@ int dispatch8(GroupArgs& p, int out_dtype, int act, int bm, hipStream_t st) {
   return FLIDE_MOE_ERR_ARG;
 }
 
+// The prefill and decode kernels address the gathered activation rows and one expert's weight rows as
+// 32-bit byte offsets from uniform 64-bit bases: the last row a pair can name (row max_row of a, row
+// N - 1 of an expert) must end below 4 GiB from its base.
+bool offsets_fit_32(long long sa, long long max_row, long long sbn, int N, int K, int eb) {
+  const long long lim = 0xFFFFFFFFLL;
+  return (max_row * sa + K) * eb <= lim && ((long long)(N - 1) * sbn + K) * eb <= lim;
+}
+
 }  // namespace
 
 extern "C" int flide_moe_grouped(const void* a, long long sa, int a_dtype, const void* w,
@@ -756,6 +741,8 @@ extern "C" int flide_moe_grouped(const void* a, long long sa, int a_dtype, const
   if (act != ACT_NONE && N % 2) return FLIDE_MOE_ERR_ARG;
   if (((uintptr_t)a | (uintptr_t)w) & 15) return FLIDE_MOE_ERR_ARG;
   if (nbm == 0 || n_pairs == 0) return FLIDE_MOE_OK;
+  if (!offsets_fit_32(sa, by_token ? (n_pairs - 1) / topk : n_pairs - 1, sbn, N, K, 2))
+    return FLIDE_MOE_ERR_ARG;
   GroupArgs p{};
   p.a = a; p.sa = sa; p.w = w; p.sbe = sbe; p.sbn = sbn;
   p.N = N; p.K = K; p.out = out; p.sc = sc; p.weights = weights;
@@ -785,6 +772,8 @@ extern "C" int flide_moe_grouped_fp8(const void* a, long long sa, const float* a
   if (act != ACT_NONE && N % 2) return FLIDE_MOE_ERR_ARG;
   if (((uintptr_t)a | (uintptr_t)w) & 15) return FLIDE_MOE_ERR_ARG;
   if (nbm == 0 || n_pairs == 0) return FLIDE_MOE_OK;
+  if (!offsets_fit_32(sa, by_token ? (n_pairs - 1) / topk : n_pairs - 1, sbn, N, K, 1))
+    return FLIDE_MOE_ERR_ARG;
   GroupArgs p{};
   p.a = a; p.sa = sa; p.w = w; p.sbe = sbe; p.sbn = sbn;
   p.a_scale = a_scale; p.w_scale = w_scale; p.sse = sse;

@@ -51,8 +51,9 @@ def _tile(t: tuple | None) -> tuple[int, int, int, int, int]:
 
 
 def router(x: torch.Tensor, wr: torch.Tensor, wg: torch.Tensor | None = None):
-    """(router logits [T, E], shared expert gate logits [T, 1] or None without `wg`) for rows x [T, H], both
-    in float32 (moe.py:152-169)."""
+    """Scores every expert for each token: returns float32 logits [T, E] = x @ wr^T and, when `wg` [H] is
+    given, the shared-expert gate logit x @ wg as [T, 1] (else None). Both sums stay in float32 end to end
+    (moe.py:152-169)."""
     dev = _hip.require_gpu(x, wr, wg)
     if x.stride(-1) != 1:
         x = x.contiguous()
@@ -143,7 +144,12 @@ def align(ids: torch.Tensor, experts: int, bm: int = BM, counts: torch.Tensor | 
     return rows, blocks, used
 
 
-def _grouped_common(a, w, out, rows, blocks, used, weights):
+def _grouped_common(a, w, out, rows, blocks, used, weights, bm):
+    if rows.numel() != blocks.numel() * bm:
+        raise ValueError(f"rows ({rows.numel()}) must hold blocks ({blocks.numel()}) x the tile's {bm} rows: "
+                         "pass the tile align padded with")
+    if rows.dtype != torch.int32 or blocks.dtype != torch.int32 or used.dtype != torch.int32:
+        raise TypeError("rows, blocks and used are align's int32 outputs")
     if w.stride(-1) != 1:
         w = w.contiguous()
     if a.stride(-1) != 1:
@@ -159,12 +165,13 @@ def _grouped_common(a, w, out, rows, blocks, used, weights):
 
 def grouped(a: torch.Tensor, w: torch.Tensor, out: torch.Tensor, rows, blocks, used, topk: int, by_token: bool,
             weights: torch.Tensor | None = None, tile: tuple | None = None, act: int = _hip.ACT_NONE) -> torch.Tensor:
-    """out[pair] = a[token of pair or pair] @ w[expert of pair].T, times the pair's weight when given
-    (moe.py:286-299). `tile[0]` must be the block rows `align` padded with. `act` (an extension) fuses
-    GeGLU/SwiGLU of the gate and up halves into the epilogue: out then has w.shape[1] // 2 columns."""
+    """For every pair p that `align` placed: out[p] = a[r] @ w[e].T with e the block's expert and r the
+    pair's token (by_token) or p itself, scaled by weights[p] when weights are given (moe.py:286-299).
+    `tile[0]` must equal the bm passed to `align`. `act` (an extension) applies GeGLU or SwiGLU to the gate
+    and up halves inside the epilogue, so out has w.shape[1] // 2 columns."""
     dev = _hip.require_gpu(a, w, out, rows, blocks, used, weights)
     bm, bn = _tile(tile)[:2]
-    a, w, weights = _grouped_common(a, w, out, rows, blocks, used, weights)
+    a, w, weights = _grouped_common(a, w, out, rows, blocks, used, weights, bm)
     n_pairs = out.shape[0]
     N, KD = w.shape[1], w.shape[2]
     _hip.call("flide_moe_grouped", a.data_ptr(), a.stride(0), _hip.dtype_code(a.dtype), w.data_ptr(), w.stride(0),
@@ -185,7 +192,7 @@ def grouped_fp8(a: torch.Tensor, w: torch.Tensor, w_scale: torch.Tensor, out: to
     bm, bn = _tile(tile)[:2]
     if a.dtype == torch.float8_e4m3fn:
         raise TypeError("grouped_fp8 quantises its input itself; pass the 16-bit rows")
-    a, w, weights = _grouped_common(a, w, out, rows, blocks, used, weights)
+    a, w, weights = _grouped_common(a, w, out, rows, blocks, used, weights, bm)
     aq, sa = quantize_tokens(a)
     w_scale = w_scale.contiguous()
     n_pairs = out.shape[0]
@@ -199,8 +206,9 @@ def grouped_fp8(a: torch.Tensor, w: torch.Tensor, w_scale: torch.Tensor, out: to
 
 @torch.no_grad()
 def quantize_experts(w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-    """Experts [E, N, K] -> float8 [E, N, K] and float32 scales [E, N] with w ~ q * scale (amax / 448 per
-    row), all experts in one launch (moe.py:321-333)."""
+    """Quantises expert weights [E, N, K] row by row: float8 codes [E, N, K] and float32 scales [E, N]
+    (each row's amax / 448), so that q * scale approximates w; every expert goes through one launch
+    (moe.py:321-333)."""
     from .fp8 import quantize_rows
 
     E, N, K = w.shape
@@ -210,6 +218,7 @@ def quantize_experts(w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
 
 # --- recognising the activation between the two products -----------------------------------------
 _ACT_CACHE: dict = {}
+_ACT_CACHE_MAX = 256
 
 
 def _guess_act(act) -> int:
@@ -227,31 +236,60 @@ def _guess_act(act) -> int:
     return _hip.ACT_NONE
 
 
+def _act_key(act):
+    """(key, objects the key names by id) for an activation callable: its code object, what its closure
+    cells hold and what the globals it names resolve to. Two closures of one code over different
+    callables or constants get different keys; a fresh lambda over the same helper (Gemma builds one per
+    call) gets the same key. The objects are kept alive beside the verdict, so their ids stay unique."""
+    code = getattr(act, "__code__", None)
+    if code is None:
+        return ("obj", id(act)), (act,)
+    held = [c.cell_contents for c in (act.__closure__ or ()) if _cell_full(c)]
+    glb = getattr(act, "__globals__", {})
+    held += [glb[n] for n in code.co_names if n in glb]
+    held += list(act.__defaults__ or ())
+    return (code, tuple(id(o) for o in held)), tuple(held)
+
+
+def _cell_full(cell) -> bool:
+    try:
+        cell.cell_contents
+    except ValueError:
+        return False
+    return True
+
+
 def _act_kind(act, device, dtype) -> int:
     """FLIDE_ACT_GEGLU when act(gu, n) is GELU-tanh(gu[:, :n]) * gu[:, n:], FLIDE_ACT_SWIGLU when it is
     silu(gu[:, :n]) * gu[:, n:], else FLIDE_ACT_NONE (the callable then runs between the products).
-    A callable is recognised by the names it calls (Gemma passes a fresh lambda over `_geglu` each call,
-    flide/backbones/gemma4/fused.py:238) and, outside graph capture, confirmed once per code object by
-    running it next to the fused formula on a small probe."""
-    key = getattr(act, "__code__", act)
+    A guess from the names the callable calls is confirmed, outside graph capture, by running it next to
+    the fused formula on a probe (values up to +-40, within one 16-bit rounding of the formula); the
+    verdict is cached per _act_key. During capture an unconfirmed callable runs unfused (that path
+    captures too)."""
+    key, held = _act_key(act)
     hit = _ACT_CACHE.get(key)
     if hit is not None:
-        return hit
+        return hit[0]
     guess = _guess_act(act)
     if guess == _hip.ACT_NONE or torch.cuda.is_current_stream_capturing():
-        return guess
+        return _hip.ACT_NONE
     g = torch.Generator(device="cpu").manual_seed(1234)
-    gu = (torch.randn(8, 64, generator=g) * 2).to(device=device, dtype=dtype)
+    gu = torch.randn(16, 64, generator=g) * 3
+    gu[0, :32] = torch.linspace(-40, 40, 32)
+    gu[1, 32:] = torch.linspace(-40, 40, 32)
+    gu = gu.to(device=device, dtype=dtype)
     try:
         got = act(gu, 32)
     except Exception:  # noqa: BLE001 - a callable that cannot take the probe is not one we fuse
         got = None
     ok = False
-    if got is not None and tuple(got.shape) == (8, 32):
-        ref = pointwise._gated(gu[:, :32], gu[:, 32:], guess)
-        ok = bool(torch.allclose(got.float(), ref.float(), rtol=2e-2, atol=2e-2))
+    if isinstance(got, torch.Tensor) and tuple(got.shape) == (16, 32):
+        ref = pointwise._gated(gu[:, :32], gu[:, 32:], guess).float()
+        ok = bool(torch.allclose(got.float(), ref, rtol=2 ** -7, atol=1e-5))
     kind = guess if ok else _hip.ACT_NONE
-    _ACT_CACHE[key] = kind
+    if len(_ACT_CACHE) >= _ACT_CACHE_MAX:
+        _ACT_CACHE.clear()
+    _ACT_CACHE[key] = (kind, held)
     return kind
 
 
@@ -261,6 +299,10 @@ def experts(x: torch.Tensor, w: dict, top: torch.Tensor, ids: torch.Tensor, act)
     ones (moe.py:336-353). `act(gu, inter)` is the activation of the gate and up halves; GeGLU and SwiGLU
     run fused in the gate/up product, anything else runs as given between two grouped products."""
     dev = _hip.require_gpu(x, top, ids)
+    if ids.dtype != torch.int32 or top.dtype != torch.float32:
+        raise TypeError(f"experts takes route's float32 weights and int32 ids; got {top.dtype} and {ids.dtype}")
+    if top.shape != ids.shape or top.shape[0] != x.shape[0]:
+        raise ValueError(f"routing shapes {tuple(top.shape)}, {tuple(ids.shape)} do not match x {tuple(x.shape)}")
     T, H = x.shape
     K, I = top.shape[1], w["inter"]
     wgu, wd = w["experts"], w["experts_down"]
@@ -295,8 +337,8 @@ def experts(x: torch.Tensor, w: dict, top: torch.Tensor, ids: torch.Tensor, act)
 
 
 def combine(y: torch.Tensor, shared: torch.Tensor, gate: torch.Tensor, k: int) -> torch.Tensor:
-    """sum over each token's k expert rows of y [T * k, H] plus the shared expert's output [T, H] scaled by the
-    sigmoid of its gate logit [T, 1], summed in float32 and rounded once (moe.py:269-277)."""
+    """Qwen's combine: out[t] = sum_j y[t*k + j] + sigmoid(gate[t]) * shared[t] for y [T*k, H], shared
+    [T, H] and gate logits [T, 1]; float32 arithmetic, one rounding to shared's dtype (moe.py:269-277)."""
     dev = _hip.require_gpu(y, shared, gate)
     T, H = shared.shape
     shared = shared.contiguous()
@@ -317,7 +359,7 @@ def moe(x: torch.Tensor, w: dict, mm, swiglu) -> torch.Tensor:
     wr, wg = w["router"], w["shared_gate"]
     if isinstance(wr, torch.Tensor) and isinstance(wg, torch.Tensor):
         logits, gate = router(x, wr, wg)
-    else:   # an adapter on the router or the gate: their own products
+    else:   # LoRA-wrapped weights are not plain tensors: the backbone's mm computes them
         logits, gate = mm(x, wr), mm(x, wg)
     top, ids = route(logits, K)
     y = experts(x, w, top, ids, swiglu)
@@ -358,8 +400,9 @@ def combine_norm_sandwich(y: torch.Tensor, dense: torch.Tensor, w1: torch.Tensor
 
 def combine_norm(y: torch.Tensor, dense: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, k: int,
                  eps: float) -> torch.Tensor:
-    """Gemma 4's two feed-forward branches joined: RMSNorm(dense) * w1 + RMSNorm(sum over each token's k
-    expert rows of y [T * k, H]) * w2, in float32 and rounded once to dense's dtype (moe.py:386-395)."""
+    """Joins Gemma 4's dense-MLP output and its experts: out[t] = RMS(dense[t]) * w1 + RMS(s[t]) * w2 with
+    s[t] = sum_j y[t*k + j] taken in slot order; float32 arithmetic, rounded once to dense's dtype
+    (moe.py:386-395)."""
     dev = _hip.require_gpu(y, dense, w1, w2)
     T, H = dense.shape
     out = torch.empty_like(dense)

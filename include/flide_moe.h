@@ -120,7 +120,9 @@ int flide_moe_align(const int* ids, int n, int E, int bm, int* rows, int* blocks
  * same dtype (strides sbe, sbn); out: [n_pairs, N or N/2] (out_dtype F32 or a_dtype, row stride sc);
  * weights: [n_pairs] float32 or NULL. nbm = total / bm is the static block count (grid bound).
  * bm must be the value align padded with; bn selects the column tile (0 = default).
- * K must be a multiple of 8 and rows 16-byte aligned.
+ * K must be a multiple of 8 and rows 16-byte aligned. The last a row a pair names and the last row of
+ * one expert's weights must each end within 4 GiB of their base (the kernels use 32-bit byte offsets);
+ * larger operands return FLIDE_MOE_ERR_ARG.
  */
 int flide_moe_grouped(const void* a, long long sa, int a_dtype, const void* w, long long sbe,
                       long long sbn, int N, int K, void* out, long long sc, int out_dtype,
@@ -135,6 +137,7 @@ int flide_moe_grouped(const void* a, long long sa, int a_dtype, const void* w, l
  * with the same fused-activation option as flide_moe_grouped (the activation reads gu rounded to
  * out_dtype). a: [*, K] e4m3 (row stride sa); a_scale: [*] float32; w: [E, N, K] e4m3 (strides sbe,
  * sbn); w_scale: [E, N] float32 (row stride sse); out: out_dtype BF16, F16 or F32. K % 16 == 0.
+ * The same 4 GiB operand limit as flide_moe_grouped.
  */
 int flide_moe_grouped_fp8(const void* a, long long sa, const float* a_scale, const void* w,
                           long long sbe, long long sbn, const float* w_scale, long long sse, int N,

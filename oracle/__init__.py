@@ -8,5 +8,5 @@ Modules:
   moe_oracle   numpy restatement of flide/kernels/moe.py, fp8.py and the pointwise pieces on the path
   cpu_path     torch-CPU restatement of the reference's eager CPU torch path (transformers' Gemma 4
                router + experts loop), used as the timed CPU baseline
-  inputs       seeded synthetic inputs for the five BASELINE configurations
+
 """

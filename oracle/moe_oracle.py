@@ -340,15 +340,22 @@ def combine_sum(y, k: int, dtype: str = "bf16") -> np.ndarray:
 # ----------------------------------------------------------------------------------------------------
 # whole layers
 # ----------------------------------------------------------------------------------------------------
-def gemma_moe(h, dense, wd: dict, eps: float, dtype: str = "bf16") -> np.ndarray:
+def gemma_moe(h, dense, wd: dict, eps: float, dtype: str = "bf16", tokens=None, parts: dict | None = None):
     """flide/backbones/gemma4/fused.py:231-240 (FusedDecoder._moe): rms_norm -> router -> route(scale)
-    -> rms_norm -> experts(GeGLU) -> combine_norm."""
+    -> rms_norm -> experts(GeGLU) -> combine_norm. `tokens` (ascending indices) restricts the expert
+    products and the combine to those tokens' rows (routing still runs over the whole batch) and the
+    result to those rows. `parts`, when given, receives the intermediate logits, top, ids and x2."""
     r = rms_norm(h, wd["router_norm"], eps, dtype=dtype)
     logits, _ = router(r, wd["router"])
-    top, ids = route(logits, wd["topk"], wd["expert_scale"])
+    k = wd["topk"]
+    top, ids = route(logits, k, wd["expert_scale"])
     x2 = rms_norm(h, wd["pre_norm_2"], eps, dtype=dtype)
-    y = experts(x2, wd["experts"], wd["experts_down"], top, ids, wd["inter"], "geglu", dtype)
-    return combine_norm(y, dense, wd["post_norm_1"], wd["post_norm_2"], wd["topk"], eps, dtype)
+    if parts is not None:
+        parts.update(logits=logits, top=top, ids=ids, x2=x2)
+    tok = np.arange(h.shape[0]) if tokens is None else np.asarray(tokens, np.int64)
+    pairs = (tok[:, None] * k + np.arange(k)[None, :]).reshape(-1)
+    y = experts(x2, wd["experts"], wd["experts_down"], top, ids, wd["inter"], "geglu", dtype, pairs=pairs)
+    return combine_norm(y[pairs], np.asarray(dense)[tok], wd["post_norm_1"], wd["post_norm_2"], k, eps, dtype)
 
 
 def qwen_moe(x, wd: dict, dtype: str = "bf16") -> np.ndarray:

@@ -103,13 +103,14 @@ def test_align_skewed_and_empty():
     _check_align(ids, 16, 64)
 
 
-@pytest.mark.parametrize("cfg", [1, 2, 4])
+@pytest.mark.parametrize("cfg", [1, 2, 3, 4])
 def test_align_configs_exact(cfg):
-    print(f"align cfg{cfg}", flush=True)
+    """Every config's routing at the tile its experts call pads with (cfg3: the float8 tile)."""
     d = logits_only(cfg)
     c = d["cfg"]
     _, rids = orc.route(d["logits"].numpy(), c.k)
-    bm = _moe().tile(c.pairs, False)[0]
+    bm = _moe().tile(c.pairs, c.dtype == "fp8")[0]
+    print(f"align cfg{cfg} bm={bm}", flush=True)
     _check_align(rids, c.E, bm)
 
 
@@ -167,6 +168,41 @@ def test_grouped_gated_tails(bm, act, dt):
     ref = orc.geglu(gu[:, :half], gu[:, half:], odt) if act == "geglu" else orc.swiglu(gu, half, odt)
     assert not np.isnan(np32(out)).any(), "a valid pair's row was not written"
     assert_close(np32(out), ref, REL_BF16, f"gated bm={bm} {act}")
+
+
+@pytest.mark.parametrize("bm", [16, 32, 64, 128, 256])
+@pytest.mark.parametrize("act", ["geglu", "swiglu"])
+@pytest.mark.parametrize("odt", [torch.bfloat16, torch.float16])
+def test_grouped_fp8_gated_tails(bm, act, odt):
+    """The fused float8 gate/up epilogue on every tile (bm 128 is what 4096-16384 tokens run: 8 waves,
+    BN 256, 3 stages) against the dequantised computation: half = 300 output columns (three column
+    tiles of 128 and a tail of 44 at BN 256), K = 400 (three 128-wide stages and a 16-wide tail, long
+    enough for every tile's ring), experts holding 1-3 blocks, rows by token. The oracle rounds gu to
+    the output type before the activation, as the reference stores gu (moe.py:345-350)."""
+    print(f"grouped fp8 gated bm={bm} {act} {odt}", flush=True)
+    from flide_amd import _hip
+
+    moe = _moe()
+    g = torch.Generator().manual_seed(300 + bm)
+    T, E, k, half, K = 700, 6, 2, 300, 400
+    _, ids = orc.route(torch.randn(T, E, generator=g).numpy(), k)
+    x = torch.randn(T, K, generator=g).to(odt)
+    w = (torch.randn(E, 2 * half, K, generator=g) * 0.05).to(torch.bfloat16)
+    qw, sw = orc.quantize_experts(np32(w))
+    qx, sx = orc.quantize_tokens(np32(x))
+    wq = torch.from_numpy(orc.e4m3fn_encode(qw)).view(torch.float8_e4m3fn).to(DEV)
+    rows, blocks, used = moe.align(torch.from_numpy(ids).to(DEV), E, bm)
+    out = torch.full((T * k, half), float("nan"), device=DEV, dtype=odt)
+    code = _hip.ACT_GEGLU if act == "geglu" else _hip.ACT_SWIGLU
+    moe.grouped_fp8(x.to(DEV), wq, torch.from_numpy(sw).to(DEV), out, rows, blocks, used, k, True,
+                    tile=(bm, 128, 4, 2), act=code)
+    al = orc.align(ids, E, bm)
+    odn = "bf16" if odt == torch.bfloat16 else "f16"
+    gu = orc.grouped(qx * sx, qw * sw[:, :, None], al["rows"], al["blocks"], al["used"], T * k, k, True, bm=bm,
+                     out_dtype=odn)
+    ref = orc.geglu(gu[:, :half], gu[:, half:], odn) if act == "geglu" else orc.swiglu(gu, half, odn)
+    assert not np.isnan(np32(out)).any(), "a valid pair's row was not written"
+    assert_close(np32(out), ref, REL_BF16, f"fp8 gated bm={bm} {act}")
 
 
 @pytest.mark.parametrize("bm", [16, 32, 64, 128, 256])

@@ -381,3 +381,132 @@ def test_route_invariant_to_expert_relabelling(perm):
     _, ids = orc.route(logits, 2)
     _, ids_p = orc.route(logits[:, p], 2)
     np.testing.assert_array_equal(p[ids_p], ids)
+
+
+# --------------------------------------------------------------------------------------------------
+# grouped, the router's shared-expert gate, the zero-centred norm and Qwen's layer
+# --------------------------------------------------------------------------------------------------
+def _grouped_brute(a, w, ids, topk, by_token, weights, dtype):
+    """out[p] for every pair p, one dot product at a time in Python floats (float64, K in order), the
+    expert taken straight from the ids (not from align's blocks), times weights[p], rounded once."""
+    flat = np.asarray(ids).reshape(-1)
+    n, N = flat.size, w.shape[1]
+    out = np.empty((n, N), np.float32)
+    for p in range(n):
+        src = p // topk if by_token else p
+        e = int(flat[p])
+        for c in range(N):
+            s = 0.0
+            for kk in range(a.shape[1]):
+                s += float(a[src, kk]) * float(w[e, c, kk])
+            if weights is not None:
+                s *= float(weights[p])
+            out[p, c] = s
+    return orc._round(out, dtype)
+
+
+@pytest.mark.parametrize("bm,by_token,mul_w,dtype", [(4, True, False, "bf16"), (8, False, True, "fp32"),
+                                                    (3, True, True, "f16"), (16, False, False, "bf16")])
+def test_grouped_brute_force(bm, by_token, mul_w, dtype):
+    """grouped over align's padded layout equals a per-pair loop that never looks at the layout: every
+    pair's row, every padding row untouched, any tile."""
+    rng = np.random.default_rng(bm + 10 * by_token)
+    T, E, k, N, K = 23, 5, 2, 7, 12
+    ids = np.stack([rng.permutation(E)[:k] for _ in range(T)])
+    ids[:6] = [3, 1]                    # one expert busier than a block, expert 4 rare
+    a = orc.bf16_round(rng.standard_normal((T if by_token else T * k, K)).astype(np.float32))
+    w = orc.bf16_round(rng.standard_normal((E, N, K)).astype(np.float32))
+    wts = rng.random(T * k).astype(np.float32) if mul_w else None
+    al = orc.align(ids, E, bm)
+    got = orc.grouped(a, w, al["rows"], al["blocks"], al["used"], T * k, k, by_token, wts, bm=bm, out_dtype=dtype)
+    ref = _grouped_brute(a, w, ids, k, by_token, wts, dtype)
+    np.testing.assert_allclose(got, ref, rtol=2 ** -22, atol=0)
+    # a row no pair names (past n_pairs) is never written
+    out = np.full((T * k + 3, N), np.nan, np.float32)
+    orc.grouped(a, w, al["rows"], al["blocks"], al["used"], T * k, k, by_token, wts, bm=bm, out_dtype=dtype, out=out)
+    assert np.isnan(out[T * k:]).all() and not np.isnan(out[:T * k]).any()
+
+
+@pytest.mark.parametrize("act", ["geglu", "swiglu"])
+@pytest.mark.parametrize("bm", [4, 16])
+def test_grouped_composition_is_experts(act, bm):
+    """align -> grouped(gate/up, by token) -> act -> grouped(down, x weight) -- the reference's experts()
+    (moe.py:336-353) -- gives orc.experts' bits (which transformers' Gemma4TextExperts pins)."""
+    rng = np.random.default_rng(20 + bm)
+    T, E, k, H, I = 31, 6, 3, 40, 24
+    ids = np.stack([rng.permutation(E)[:k] for _ in range(T)])
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    top, ids = orc.route(logits, k)
+    x = orc.bf16_round(rng.standard_normal((T, H)).astype(np.float32))
+    wgu = orc.bf16_round((rng.standard_normal((E, 2 * I, H)) * 0.2).astype(np.float32))
+    wd = orc.bf16_round((rng.standard_normal((E, H, I)) * 0.2).astype(np.float32))
+    al = orc.align(ids, E, bm)
+    gu = orc.grouped(x, wgu, al["rows"], al["blocks"], al["used"], T * k, k, True, bm=bm, out_dtype="bf16")
+    a = orc.geglu(gu[:, :I], gu[:, I:], "bf16") if act == "geglu" else orc.swiglu(gu, I, "bf16")
+    y = orc.grouped(a, wd, al["rows"], al["blocks"], al["used"], T * k, k, False, top.reshape(-1), bm=bm,
+                    out_dtype="fp32")
+    ref = orc.experts(x, wgu, wd, top, ids, I, act, "bf16")
+    np.testing.assert_array_equal(y, ref)
+
+
+def test_router_gate_term_matches_linear():
+    """router's logits and its shared-expert gate logit (moe.py:152-169) against torch's F.linear in
+    float64 (Qwen3_5MoeTopKRouter and shared_expert_gate are both F.linear)."""
+    rng = np.random.default_rng(30)
+    x = rng.standard_normal((17, 96)).astype(np.float32)
+    wr = rng.standard_normal((12, 96)).astype(np.float32)
+    wg = rng.standard_normal(96).astype(np.float32)
+    logits, gate = orc.router(x, wr, wg)
+    xt = torch.from_numpy(x).double()
+    np.testing.assert_allclose(logits, F.linear(xt, torch.from_numpy(wr).double()).float().numpy(), rtol=1e-6)
+    np.testing.assert_allclose(gate, F.linear(xt, torch.from_numpy(wg).double()[None]).float().numpy(), rtol=1e-6)
+    assert gate.shape == (17, 1) and orc.router(x, wr)[1] is None
+
+
+def test_rms_norm_offset_matches_qwen():
+    """rms_norm(offset=True), the zero-centred weight (pointwise.py:21-49), against transformers'
+    Qwen3_5MoeRMSNorm (float32 math, (1 + w), rounded to the input's dtype): within one bf16 rounding of
+    each other (float32 vs float64 intermediates), and equal almost everywhere."""
+    from transformers.models.qwen3_5_moe.modeling_qwen3_5_moe import Qwen3_5MoeRMSNorm
+
+    torch.manual_seed(31)
+    N = 256
+    m = Qwen3_5MoeRMSNorm(N, eps=1e-6)
+    with torch.no_grad():
+        m.weight.copy_(torch.randn(N) * 0.3)
+    x = (torch.randn(50, N) * 3).to(torch.bfloat16)
+    with torch.no_grad():
+        ref = m(x).float().numpy()
+    got = orc.rms_norm(x.float().numpy(), m.weight.detach().numpy(), 1e-6, offset=True, dtype="bf16")
+    np.testing.assert_allclose(got, ref, rtol=2 ** -7, atol=1e-6)
+    assert (got == ref).mean() > 0.99
+    # offset=False is a different formula: it must not pass for this weight
+    plain = orc.rms_norm(x.float().numpy(), m.weight.detach().numpy(), 1e-6, offset=False, dtype="bf16")
+    assert not np.allclose(plain, ref, rtol=1e-2)
+
+
+def test_qwen_moe_matches_transformers_block():
+    """qwen_moe (moe.py:356-369) against transformers' Qwen3_5MoeSparseMoeBlock in float32: router and
+    softmax top-k, the SwiGLU experts loop, the shared expert and its sigmoid gate."""
+    from transformers.models.qwen3_5_moe.configuration_qwen3_5_moe import Qwen3_5MoeTextConfig
+    from transformers.models.qwen3_5_moe.modeling_qwen3_5_moe import Qwen3_5MoeSparseMoeBlock
+
+    torch.manual_seed(32)
+    H, E, k, I, SI, T = 64, 8, 2, 32, 48, 30
+    cfg = Qwen3_5MoeTextConfig(hidden_size=H, num_experts=E, num_experts_per_tok=k, moe_intermediate_size=I,
+                               shared_expert_intermediate_size=SI, hidden_act="silu")
+    blk = Qwen3_5MoeSparseMoeBlock(cfg).float()
+    with torch.no_grad():
+        for p in blk.parameters():
+            p.normal_(0, 0.2)
+    x = torch.randn(1, T, H)
+    with torch.no_grad():
+        ref = blk(x)[0].numpy()
+    se = blk.shared_expert
+    wd = {"topk": k, "inter": I, "shared_inter": SI,
+          "router": blk.gate.weight.detach().numpy(), "shared_gate": blk.shared_expert_gate.weight.detach().numpy(),
+          "experts": blk.experts.gate_up_proj.detach().numpy(), "experts_down": blk.experts.down_proj.detach().numpy(),
+          "shared_gate_up": torch.cat([se.gate_proj.weight, se.up_proj.weight]).detach().numpy(),
+          "shared_down": se.down_proj.weight.detach().numpy()}
+    got = orc.qwen_moe(x[0].numpy(), wd, "fp32")
+    np.testing.assert_allclose(got, ref, rtol=1e-4, atol=1e-5)
