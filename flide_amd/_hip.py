@@ -45,6 +45,7 @@ SIGNATURES: dict[str, list] = {
     "flide_moe_experts_workspace": [_I, _I, _I, _I, _I, _I, _I],
     "flide_moe_experts": [_P, _L, _I, _I, _I, _P, _P, _I, _P, _P, _P, _P, _I, _I, _P, _I, _I, _I, _P,
                           c_size_t, _P],
+    "flide_moe_experts_noalloc": [_P, _L, _I, _I, _I, _P, _P, _I, _P, _P, _P, _P, _I, _I, _P, _I, _I, _I, _P],
 }
 _RESTYPES = {
     "flide_moe_strerror": ctypes.c_char_p,

@@ -2,7 +2,10 @@
 // activation, down product times the routing weight; plus the float8 variant with its two
 // per-row quantizations (flide/kernels/moe.py:345-349, fp8.py:29-53). All scratch lives in the
 // caller's workspace, carved in the fixed order below, so the call allocates nothing and can be
-// captured into a HIP graph.
+// captured into a HIP graph. flide_moe_experts_noalloc carves the same layout out of a static device
+// array instead, for callers that cannot allocate at all.
+#include <mutex>
+
 #include "common.hpp"
 
 namespace {
@@ -41,6 +44,9 @@ extern "C" const char* flide_moe_strerror(int rc) {
     case FLIDE_MOE_ERR_ARG: return "invalid argument (size, stride, alignment or dtype)";
     case FLIDE_MOE_ERR_WORKSPACE: return "workspace too small";
     case FLIDE_MOE_ERR_TILE: return "no kernel compiled for this tile shape";
+    case FLIDE_MOE_ERR_SCRATCH:
+      return "problem larger than the allocation-free entry point's static scratch "
+             "(FLIDE_MOE_NOALLOC_SCRATCH_BYTES): call flide_moe_experts with a workspace";
     default:
       if (rc >= FLIDE_MOE_ERR_HIP_BASE) return hipGetErrorString((hipError_t)(rc - FLIDE_MOE_ERR_HIP_BASE));
       return "unknown error";
@@ -54,20 +60,23 @@ extern "C" size_t flide_moe_experts_workspace(int T, int k, int E, int H, int I,
   return layout(T, k, E, H, I, bm, fp8).total;
 }
 
-extern "C" int flide_moe_experts(const void* x, long long sx, int x_dtype, int T, int H,
-                                 const float* top, const int* ids, int k, const void* w_gu,
-                                 const void* w_d, const float* w_scale_gu, const float* w_scale_d,
-                                 int E, int I, void* y, int act, int bm, int bn, void* workspace,
-                                 size_t workspace_bytes, flide_stream_t stream) {
-  if (T < 0 || H <= 0 || k <= 0 || E <= 0 || I <= 0) return FLIDE_MOE_ERR_ARG;
+namespace {
+
+// Both entry points: arguments checked, then `ws` (ws_bytes >= layout().total) carved and the launches
+// enqueued. Nothing in the layout needs to start zeroed:
+// align writes its histograms before reading them, and the products write every row they later read.
+int run_experts(const void* x, long long sx, int x_dtype, int T, int H, const float* top, const int* ids,
+                int k, const void* w_gu, const void* w_d, const float* w_scale_gu, const float* w_scale_d,
+                int E, int I, void* y, int act, int bm, int bn, char* ws, size_t ws_bytes,
+                flide_stream_t stream) {
+  if (T < 0 || H <= 0 || k <= 0 || E <= 0 || I <= 0 || bm <= 0) return FLIDE_MOE_ERR_ARG;
   if (x_dtype != FLIDE_BF16 && x_dtype != FLIDE_F16) return FLIDE_MOE_ERR_ARG;
   if (act != ACT_GEGLU && act != ACT_SWIGLU) return FLIDE_MOE_ERR_ARG;
   const int fp8 = w_scale_gu != nullptr;
   if (fp8 != (w_scale_d != nullptr)) return FLIDE_MOE_ERR_ARG;
   if (T == 0) return FLIDE_MOE_OK;
   const ExpertsLayout L = layout(T, k, E, H, I, bm, fp8);
-  if (workspace_bytes < L.total) return FLIDE_MOE_ERR_WORKSPACE;
-  char* ws = (char*)workspace;
+  if (ws_bytes < L.total) return FLIDE_MOE_ERR_WORKSPACE;
   int* rows = (int*)(ws + L.rows);
   int* blocks = (int*)(ws + L.blocks);
   int* used = (int*)(ws + L.used);
@@ -100,4 +109,67 @@ extern "C" int flide_moe_experts(const void* x, long long sx, int x_dtype, int T
   return flide_moe_grouped_fp8(qa, I, sas, w_d, (long long)H * I, I, w_scale_d, H, H, I, y, H,
                                x_dtype, top, rows, blocks, used, n, nbm, k, 0, ACT_NONE, bm, bn,
                                stream);
+}
+
+// The allocation-free entry point's scratch: one copy of this array per device, resident from module
+// load until the process ends. Host code never passes `scratch` itself (on the host it names a
+// stand-in, not device memory): each device's address comes from hipGetSymbolAddress, taken once per
+// device with that device current, and only that address reaches the kernels.
+static __device__ __align__(256) char scratch[FLIDE_MOE_NOALLOC_SCRATCH_BYTES];
+
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void* g_scratch[MAX_DEVICES];
+
+// this device's address of `scratch` (the stream's device, or the current one for the null stream)
+int scratch_for(hipStream_t st, char** out) {
+  int cur = 0, dev = 0;
+  hipError_t e = hipGetDevice(&cur);
+  if (e != hipSuccess) return FLIDE_MOE_ERR_HIP_BASE + (int)e;
+  dev = cur;
+  if (st != nullptr) {
+    e = hipStreamGetDevice(st, &dev);
+    if (e != hipSuccess) return FLIDE_MOE_ERR_HIP_BASE + (int)e;
+  }
+  if (dev < 0 || dev >= MAX_DEVICES) return FLIDE_MOE_ERR_ARG;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch[dev] == nullptr) {
+    if (dev != cur && (e = hipSetDevice(dev)) != hipSuccess) return FLIDE_MOE_ERR_HIP_BASE + (int)e;
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    const hipError_t back = dev != cur ? hipSetDevice(cur) : hipSuccess;
+    if (e != hipSuccess) return FLIDE_MOE_ERR_HIP_BASE + (int)e;
+    if (back != hipSuccess) return FLIDE_MOE_ERR_HIP_BASE + (int)back;
+    if (p == nullptr) return FLIDE_MOE_ERR_HIP_BASE + (int)hipErrorInvalidSymbol;
+    g_scratch[dev] = p;
+  }
+  *out = (char*)g_scratch[dev];
+  return FLIDE_MOE_OK;
+}
+
+}  // namespace
+
+extern "C" int flide_moe_experts(const void* x, long long sx, int x_dtype, int T, int H,
+                                 const float* top, const int* ids, int k, const void* w_gu,
+                                 const void* w_d, const float* w_scale_gu, const float* w_scale_d,
+                                 int E, int I, void* y, int act, int bm, int bn, void* workspace,
+                                 size_t workspace_bytes, flide_stream_t stream) {
+  return run_experts(x, sx, x_dtype, T, H, top, ids, k, w_gu, w_d, w_scale_gu, w_scale_d, E, I, y, act,
+                     bm, bn, (char*)workspace, workspace_bytes, stream);
+}
+
+extern "C" int flide_moe_experts_noalloc(const void* x, long long sx, int x_dtype, int T, int H,
+                                         const float* top, const int* ids, int k, const void* w_gu,
+                                         const void* w_d, const float* w_scale_gu,
+                                         const float* w_scale_d, int E, int I, void* y, int act,
+                                         int bm, int bn, flide_stream_t stream) {
+  if (T < 0 || H <= 0 || k <= 0 || E <= 0 || I <= 0 || bm <= 0) return FLIDE_MOE_ERR_ARG;
+  if (T == 0) return FLIDE_MOE_OK;
+  const size_t need = layout(T, k, E, H, I, bm, w_scale_gu != nullptr).total;
+  if (need > FLIDE_MOE_NOALLOC_SCRATCH_BYTES) return FLIDE_MOE_ERR_SCRATCH;
+  char* ws = nullptr;
+  const int rc = scratch_for((hipStream_t)stream, &ws);
+  if (rc) return rc;
+  return run_experts(x, sx, x_dtype, T, H, top, ids, k, w_gu, w_d, w_scale_gu, w_scale_d, E, I, y, act,
+                     bm, bn, ws, FLIDE_MOE_NOALLOC_SCRATCH_BYTES, stream);
 }

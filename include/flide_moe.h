@@ -43,6 +43,7 @@ enum {
   FLIDE_MOE_ERR_ARG = 1,       /* a size, stride, pointer alignment or dtype the kernels do not take */
   FLIDE_MOE_ERR_WORKSPACE = 2, /* workspace smaller than the *_workspace query returned */
   FLIDE_MOE_ERR_TILE = 3,      /* a tile shape with no compiled kernel */
+  FLIDE_MOE_ERR_SCRATCH = 4,   /* larger than flide_moe_experts_noalloc's static scratch */
   FLIDE_MOE_ERR_HIP_BASE = 1000 /* + hipError_t of a failed launch */
 };
 
@@ -229,6 +230,28 @@ int flide_moe_experts(const void* x, long long sx, int x_dtype, int T, int H, co
                       const int* ids, int k, const void* w_gu, const void* w_d, const float* w_scale_gu,
                       const float* w_scale_d, int E, int I, void* y, int act, int bm, int bn,
                       void* workspace, size_t workspace_bytes, flide_stream_t stream);
+
+/*
+ * Bytes of device memory flide_moe_experts_noalloc keeps per GPU (a static array, resident from the
+ * library's load until the process ends).
+ */
+#define FLIDE_MOE_NOALLOC_SCRATCH_BYTES (16u << 20)
+
+/*
+ * flide_moe_experts without a workspace argument: its scratch is a static device array of
+ * FLIDE_MOE_NOALLOC_SCRATCH_BYTES per GPU, so the call allocates nothing at all (no hipMalloc, no
+ * allocating library call). No counterpart in the reference: it is for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid allocation). Same arguments,
+ * kernels and output bits as flide_moe_experts. A problem whose flide_moe_experts_workspace exceeds the
+ * scratch returns FLIDE_MOE_ERR_SCRATCH (at the Gemma 4 26B-A4B shape: about 1480 tokens with 16-bit
+ * experts, about 840 with float8 ones). Every call on one GPU uses that GPU's one array: calls that
+ * overlap on a GPU (on different streams, or from different threads) race and must be ordered by the
+ * caller. The array's contents carry over between calls; nothing in it needs to start zeroed.
+ */
+int flide_moe_experts_noalloc(const void* x, long long sx, int x_dtype, int T, int H, const float* top,
+                              const int* ids, int k, const void* w_gu, const void* w_d,
+                              const float* w_scale_gu, const float* w_scale_d, int E, int I, void* y,
+                              int act, int bm, int bn, flide_stream_t stream);
 
 #ifdef __cplusplus
 }
