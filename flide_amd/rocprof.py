@@ -4,6 +4,8 @@
     python -m flide_amd.rocprof stats  <kernel_stats.csv> <title> <command> > summary.md
     python -m flide_amd.rocprof traffic <workload> <kernel-regex> <fetch.csv> <write.csv> \\
                                          <copy_fetch.csv> <copy_write.csv> <command> > traffic.md
+    python -m flide_amd.rocprof mfma <counters.csv> <kernel-regex> <flop-per-dispatch> <peak-flop/s> \\
+                                      <title> <command> > mfma.md
 
 `copy` runs a plain device-to-device copy of COPY_BYTES (the HIP runtime's copy kernel) a few times. Under
 `rocprofv3 --pmc FETCH_SIZE` and `--pmc WRITE_SIZE` its counters give the scale from the counters'
@@ -112,9 +114,77 @@ def stats_md(path: str, title: str, command: str, top: int = 12) -> str:
     return "\n".join(out)
 
 
-def traffic_for(workload: str) -> int | None:
-    """The committed traffic figure for a bench workload (profiles/*_<workload>_traffic.md), if any."""
-    for p in sorted(PROFILES.glob(f"*_{workload}_traffic.md")):
+MFMA_COUNTERS = ("SQ_VALU_MFMA_BUSY_CYCLES", "SQ_BUSY_CYCLES", "SQ_INSTS_VALU_MFMA_MOPS_BF16",
+                 "SQ_INSTS_VALU_MFMA_MOPS_F8", "GRBM_GUI_ACTIVE")
+SIMDS, XCDS = 1024, 8   # MI355X: 256 CUs x 4 SIMDs, 8 XCDs
+
+
+def _dispatches(path: str, regex: str) -> dict[str, dict]:
+    """dispatch id -> {counter: value summed over the row's instances, "ns": kernel duration}."""
+    pat = re.compile(regex)
+    out: dict[str, dict] = {}
+    for r in _counter_rows(path):
+        if not pat.search(_kernel_name(r)):
+            continue
+        d = out.setdefault(r.get("Dispatch_Id") or r.get("Correlation_Id"), {})
+        c = r["Counter_Name"]
+        d[c] = d.get(c, 0.0) + float(r["Counter_Value"])
+        d["ns"] = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+    return out
+
+
+def mfma_md(path: str, regex: str, flop: float, peak: float, title: str, command: str) -> str:
+    """Matrix-core utilisation of the dispatches matching `regex`, medians over dispatches:
+      clock        GRBM_GUI_ACTIVE / 8 XCDs / kernel duration (the counter sums the 8 XCDs' cycles)
+      MFMA busy    SQ_VALU_MFMA_BUSY_CYCLES / (per-XCD GRBM_GUI_ACTIVE x 1024 SIMDs)
+      MFMA FLOP    SQ_INSTS_VALU_MFMA_MOPS_{BF16,F8} x 512 (what the matrix cores executed, padding included)
+    next to the launch's algorithmic FLOP (`flop`) over its duration against `peak`."""
+    ds = list(_dispatches(path, regex).values())
+    if not ds:
+        raise SystemExit(f"no dispatches matched {regex}")
+    med = lambda key: statistics.median(d.get(key, 0.0) for d in ds)   # noqa: E731
+    ns = med("ns")
+    gui = med("GRBM_GUI_ACTIVE") / XCDS
+    busy = med("SQ_VALU_MFMA_BUSY_CYCLES")
+    mops = med("SQ_INSTS_VALU_MFMA_MOPS_BF16") + med("SQ_INSTS_VALU_MFMA_MOPS_F8")
+    clock = gui / ns   # GHz
+    util = busy / (gui * SIMDS) if gui else 0.0
+    lines = [
+        f"# MFMA utilisation: {title}",
+        "",
+        f"Kernels matching `{regex}`; one rocprofv3 `--pmc` pass ({' '.join(MFMA_COUNTERS)}).",
+        "",
+        "```",
+        command,
+        "```",
+        "",
+        "| quantity | value |",
+        "|---|---|",
+        f"| dispatches | {len(ds)} |",
+        f"| duration (median, under counter collection) | {ns / 1e3:.1f} us |",
+        f"| GRBM_GUI_ACTIVE per XCD | {gui:.0f} cycles |",
+        f"| shader clock during the kernel | {clock:.2f} GHz |",
+        f"| SQ_VALU_MFMA_BUSY_CYCLES | {busy:.4g} |",
+        f"| SQ_BUSY_CYCLES | {med('SQ_BUSY_CYCLES'):.4g} |",
+        f"| **MFMA busy** (of all SIMD cycles) | **{100 * util:.1f}%** |",
+        f"| MFMA FLOP executed (MOPS x 512) | {mops * 512:.4g} |",
+        f"| algorithmic FLOP per dispatch | {flop:.4g} (executed / algorithmic = {mops * 512 / flop:.2f}) |",
+        f"| algorithmic FLOP/s at this duration | {flop / ns / 1e3:.1f} TFLOP/s = {100 * flop / ns * 1e9 / peak:.1f}% "
+        f"of {peak / 1e12:.0f} TFLOP/s |",
+        f"| peak at the measured clock (x {clock:.2f} / 2.4 GHz) | {peak / 1e12 * clock / 2.4:.0f} TFLOP/s |",
+        "",
+        f"mfma_busy: {util:.4f}",
+        f"sclk_ghz: {clock:.3f}",
+        "",
+    ]
+    return "\n".join(lines)
+
+
+def traffic_for(workload: str, kernel: str = "gate_up") -> int | None:
+    """The committed traffic figure of one product (`gate_up` or `down`) at a bench workload
+    (profiles/<kernel>_<workload>_traffic.md), if any."""
+    p = PROFILES / f"{kernel}_{workload}_traffic.md"
+    if p.exists():
         m = re.search(r"^traffic_bytes_per_dispatch: (\d+)$", p.read_text(), re.M)
         if m:
             return int(m.group(1))
@@ -133,6 +203,9 @@ def main(argv: list[str]) -> int:
         return 0
     if argv[0] == "traffic" and len(argv) == 8:
         print(traffic_md(*argv[1:]))
+        return 0
+    if argv[0] == "mfma" and len(argv) == 7:
+        print(mfma_md(argv[1], argv[2], float(argv[3]), float(argv[4]), argv[5], argv[6]))
         return 0
     print(__doc__)
     return 2

@@ -112,3 +112,24 @@ def quantize_rows_cpu(w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
         q[e] = (we / sc).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
         s[e] = sc[:, 0]
     return q, s
+
+
+def device_weights(cfg: Config | int, device, seed: int = 0) -> dict:
+    """Expert weights of `cfg`'s shape drawn on the GPU (N(0, 0.02) float32 masters from a device
+    generator seeded with `seed`, then bf16, or quantised per row to e4m3fn by this library's own
+    quantize_experts for the FP8 config): the benchmark's fast path, seconds instead of the CPU draw's
+    tens of seconds. Same distributions as make_inputs, not the same bits."""
+    from .kernels import moe
+
+    if isinstance(cfg, int):
+        cfg = CONFIGS[cfg]
+    g = torch.Generator(device=device).manual_seed(seed)
+    out = {}
+    for name, shape in (("w_gu", (cfg.E, 2 * cfg.I, cfg.H)), ("w_d", (cfg.E, cfg.H, cfg.I))):
+        w = (torch.randn(*shape, generator=g, device=device) * 0.02).to(torch.bfloat16)
+        if cfg.dtype == "fp8":
+            out[name], out[name + "_scale"] = moe.quantize_experts(w)
+        else:
+            out[name] = w
+        del w
+    return out

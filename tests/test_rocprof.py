@@ -37,11 +37,31 @@ def test_per_dispatch_sums_counter_instances(tmp_path):
 
 
 def test_committed_traffic_figures_parse():
-    # every committed traffic summary yields a positive byte count for its workload
-    files = sorted(rocprof.PROFILES.glob("*_traffic.md"))
-    assert files, "no traffic summaries under profiles/"
-    for f in files:
-        workload = next(w for w in ("cfg1_decode_bf16", "cfg2_prefill_bf16", "cfg3_fp8", "cfg4_skewed_bf16")
-                        if f.name.endswith(f"_{w}_traffic.md"))
-        assert rocprof.traffic_for(workload) > 0
+    # both products at every GPU workload have a committed summary with a positive byte count
+    for w in ("cfg1_decode_bf16", "cfg2_prefill_bf16", "cfg3_fp8", "cfg4_skewed_bf16"):
+        for kernel in ("gate_up", "down"):
+            assert rocprof.traffic_for(w, kernel) > 0, (w, kernel)
     assert rocprof.traffic_for("no_such_workload") is None
+
+
+def _write_mfma(path, rows):
+    fields = ["Dispatch_Id", "Kernel_Name", "Counter_Name", "Counter_Value", "Start_Timestamp", "End_Timestamp"]
+    with open(path, "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=fields)
+        w.writeheader()
+        for r in rows:
+            w.writerow(dict(zip(fields, r)))
+    return str(path)
+
+
+def test_mfma_summary(tmp_path):
+    # one dispatch of 1 ms: 8 XCDs x 2e6 cycles (2 GHz), MFMA busy on a quarter of the 1024 SIMDs' cycles,
+    # 1e9 bf16 MOPS (5.12e11 FLOP) for 5e11 algorithmic FLOP
+    p = _write_mfma(tmp_path / "m.csv", [
+        (1, "gemm", "GRBM_GUI_ACTIVE", 8 * 2e6, 0, 1_000_000),
+        (1, "gemm", "SQ_VALU_MFMA_BUSY_CYCLES", 0.25 * 2e6 * 1024, 0, 1_000_000),
+        (1, "gemm", "SQ_INSTS_VALU_MFMA_MOPS_BF16", 1e9, 0, 1_000_000),
+        (1, "other", "GRBM_GUI_ACTIVE", 1, 0, 5)])
+    md = rocprof.mfma_md(p, "gemm", 5e11, 2.5e15, "t", "cmd")
+    assert "mfma_busy: 0.2500" in md and "sclk_ghz: 2.000" in md
+    assert "executed / algorithmic = 1.02" in md and "500.0 TFLOP/s = 20.0% of 2500" in md
