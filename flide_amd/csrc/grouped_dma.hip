@@ -79,6 +79,20 @@ template <> struct DmaElem<Fp8Tag> {
   static constexpr int BYTES = 1;
 };
 
+// First block of the run of blocks holding expert e that contains block blk (blocks[blk] == e; align
+// writes each expert's blocks contiguously): the wave looks 64 entries back at a time until an entry
+// differs. Entries below blk are all in use, and a lane below 0 reads -1, so the loop ends.
+FLIDE_DEV int expert_first_block(const int* blocks, int blk, int e, int l) {
+  int base = blk;
+  for (;;) {
+    const int idx = base - 63 + l;
+    const int v = idx >= 0 ? blocks[idx] : -1;
+    const unsigned long long m = __ballot(v != e);
+    if (m) return base - 63 + (63 - __builtin_clzll(m)) + 1;
+    base -= 64;
+  }
+}
+
 template <typename T, typename OutT, int ACT, int BM, int BN, int WAVES_M, int WAVES_N, int NS, int ROWB, int OCC,
           int XCD_CHUNK_BLOCKS, bool NTW>
 __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void grouped_dma(GroupArgs p) {
@@ -112,27 +126,47 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void grouped_dma(Group
 
   const int tid = threadIdx.x, l = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform, in an SGPR
-  // Workgroup b runs on XCD b % 8. Items (block, column tile) are cut into chunks of CH items (a few
-  // blocks of one expert and all their column tiles) and chunk c goes to XCD c % 8, so each XCD's
-  // workgroups reuse the chunk's rows and weight tiles from that XCD's L2, and the dead items at the
-  // end of the static grid spread over all XCDs. The host rounds the grid to a multiple of 8 * CH.
-  // Inside a chunk the gated (gate/up) products run column-tile major, so the blocks that share a weight
-  // tile start back to back (16-bit at 8192 tokens: 16% less HBM fetch, 4-5% faster); the plain (down)
-  // products run block major, which measured 5% faster for them.
-  const int CH = p.ntn * XCD_CHUNK_BLOCKS;
-  const int b = blockIdx.x;
-  const int j = b >> 3;
-  const int chunk = (j / CH) * 8 + (b & 7), within = j % CH;
+  // Workgroup b runs on XCD b % 8.
   int pm, pn;
-  if constexpr (ACT != ACT_NONE) {
-    pm = chunk * XCD_CHUNK_BLOCKS + within % XCD_CHUNK_BLOCKS;
-    pn = within / XCD_CHUNK_BLOCKS;
+  if constexpr (BM >= 64) {
+    // Prefill tiles: the items (block, column tile) in use, ordered by expert, then block, then column
+    // tile, are split into 8 contiguous ranges, range x for the workgroups of XCD x. An expert's blocks
+    // and all its column tiles then run on one XCD at about the same time, so each weight tile comes
+    // from HBM once and is shared in that XCD's L2 (HBM fetch of the 16-bit gate/up product at 8192
+    // tokens: 3.1 -> 2.1-3.2 GB depending on the order inside an expert; this order measured fastest,
+    // 6-11% on the gate/up products at 4096-16384 tokens, no change on the down products).
+    const int nused = *p.used / BM;
+    const long long R = (long long)nused * p.ntn;
+    const int x = blockIdx.x & 7;
+    const long long it = R * x / 8 + (blockIdx.x >> 3);
+    if (it >= R * (x + 1) / 8) return;
+    const int blk = (int)(it / p.ntn);
+    const int ex = p.blocks[blk];
+    const int s0 = __builtin_amdgcn_readfirstlane(expert_first_block(p.blocks, blk, ex, l));
+    const int local = (int)(it - (long long)s0 * p.ntn);
+    pm = s0 + local / p.ntn;
+    pn = local % p.ntn;
   } else {
-    const int widx = chunk * CH + within;
-    pm = widx / p.ntn;
-    pn = widx % p.ntn;
+    // Decode tiles: items are cut into chunks of CH items (a few blocks of one expert and all their
+    // column tiles) and chunk c goes to XCD c % 8, so each XCD's workgroups reuse the chunk's rows and
+    // weight tiles from that XCD's L2, and the dead items at the end of the static grid spread over all
+    // XCDs (the host rounds the grid to a multiple of 8 * CH). Inside a chunk the gated (gate/up)
+    // products run column-tile major, so the blocks that share a weight tile start back to back; the
+    // plain (down) products run block major.
+    const int CH = p.ntn * XCD_CHUNK_BLOCKS;
+    const int b = blockIdx.x;
+    const int j = b >> 3;
+    const int chunk = (j / CH) * 8 + (b & 7), within = j % CH;
+    if constexpr (ACT != ACT_NONE) {
+      pm = chunk * XCD_CHUNK_BLOCKS + within % XCD_CHUNK_BLOCKS;
+      pn = within / XCD_CHUNK_BLOCKS;
+    } else {
+      const int widx = chunk * CH + within;
+      pm = widx / p.ntn;
+      pn = widx % p.ntn;
+    }
+    if (pm >= p.nbm || pm * BM >= *p.used) return;
   }
-  if (pm >= p.nbm || pm * BM >= *p.used) return;
   const long long e = p.blocks[pm];
   const int K = p.K;
   const int half = p.N / 2;
@@ -657,7 +691,9 @@ int launch_one(GroupArgs& p, hipStream_t st) {
   const int per = ACT == ACT_NONE ? BN : BN / 2;
   p.ntn = (cols + per - 1) / per;
   const int items = p.nbm * p.ntn;
-  const int round = 8 * p.ntn * XB;
+  // decode tiles: whole XCD chunks; prefill tiles: eight equal ranges of the static item count (each
+  // XCD's range of the items in use is at most that long)
+  const int round = BM >= 64 ? 8 : 8 * p.ntn * XB;
   dim3 grid((items + round - 1) / round * round), block(WM_ * WN_ * 64);
   // Non-temporal weight loads (dma16w) for every 32-row (decode) product and for the gated products of
   // larger tiles while padding fills at least half the blocks (most experts then hold one block, so each
