@@ -6,7 +6,7 @@
 // array instead, for callers that cannot allocate at all.
 #include <mutex>
 
-#include "common.hpp"
+#include "routing.hpp"
 
 namespace {
 
@@ -62,21 +62,17 @@ extern "C" size_t flide_moe_experts_workspace(int T, int k, int E, int H, int I,
 
 namespace {
 
-// Both entry points: arguments checked, then `ws` (ws_bytes >= layout().total) carved and the launches
-// enqueued. Nothing in the layout needs to start zeroed:
-// align writes its histograms before reading them, and the products write every row they later read.
-int run_experts(const void* x, long long sx, int x_dtype, int T, int H, const float* top, const int* ids,
-                int k, const void* w_gu, const void* w_d, const float* w_scale_gu, const float* w_scale_d,
-                int E, int I, void* y, int act, int bm, int bn, char* ws, size_t ws_bytes,
-                flide_stream_t stream) {
-  if (T < 0 || H <= 0 || k <= 0 || E <= 0 || I <= 0 || bm <= 0) return FLIDE_MOE_ERR_ARG;
-  if (x_dtype != FLIDE_BF16 && x_dtype != FLIDE_F16) return FLIDE_MOE_ERR_ARG;
-  if (act != ACT_GEGLU && act != ACT_SWIGLU) return FLIDE_MOE_ERR_ARG;
+bool experts_args_ok(int T, int H, int k, int E, int I, int bm, int x_dtype, int act, const float* w_scale_gu,
+                     const float* w_scale_d) {
+  return T >= 0 && H > 0 && k > 0 && E > 0 && I > 0 && bm > 0 && (x_dtype == FLIDE_BF16 || x_dtype == FLIDE_F16) &&
+         (act == ACT_GEGLU || act == ACT_SWIGLU) && ((w_scale_gu != nullptr) == (w_scale_d != nullptr));
+}
+
+// The two products on align's layout (rows, blocks, used in the workspace `ws` carved by `L`).
+int run_products(const void* x, long long sx, int x_dtype, int T, int H, const float* top, int k,
+                 const void* w_gu, const void* w_d, const float* w_scale_gu, const float* w_scale_d, int E, int I,
+                 void* y, int act, int bm, int bn, char* ws, const ExpertsLayout& L, flide_stream_t stream) {
   const int fp8 = w_scale_gu != nullptr;
-  if (fp8 != (w_scale_d != nullptr)) return FLIDE_MOE_ERR_ARG;
-  if (T == 0) return FLIDE_MOE_OK;
-  const ExpertsLayout L = layout(T, k, E, H, I, bm, fp8);
-  if (ws_bytes < L.total) return FLIDE_MOE_ERR_WORKSPACE;
   int* rows = (int*)(ws + L.rows);
   int* blocks = (int*)(ws + L.blocks);
   int* used = (int*)(ws + L.used);
@@ -84,9 +80,7 @@ int run_experts(const void* x, long long sx, int x_dtype, int T, int H, const fl
   const int n = T * k;
   const long long total = ((long long)n + (long long)E * (bm - 1) + bm - 1) / bm * bm;
   const int nbm = (int)(total / bm);
-  int rc = flide_moe_align(ids, n, E, bm, rows, blocks, used, nullptr, ws + L.hist,
-                           L.rows - L.hist, stream);
-  if (rc) return rc;
+  int rc;
   if (!fp8) {
     rc = flide_moe_grouped(x, sx, x_dtype, w_gu, (long long)2 * I * H, H, 2 * I, H, actbuf, I,
                            x_dtype, nullptr, rows, blocks, used, n, nbm, k, 1, act, bm, bn, stream);
@@ -109,6 +103,25 @@ int run_experts(const void* x, long long sx, int x_dtype, int T, int H, const fl
   return flide_moe_grouped_fp8(qa, I, sas, w_d, (long long)H * I, I, w_scale_d, H, H, I, y, H,
                                x_dtype, top, rows, blocks, used, n, nbm, k, 0, ACT_NONE, bm, bn,
                                stream);
+}
+
+// flide_moe_experts and its allocation-free twin: arguments checked, then `ws` (ws_bytes >=
+// layout().total) carved, align run and the products enqueued. Nothing in the layout needs to start
+// zeroed: align writes its histograms before reading them, and the products write every row they
+// later read.
+int run_experts(const void* x, long long sx, int x_dtype, int T, int H, const float* top, const int* ids,
+                int k, const void* w_gu, const void* w_d, const float* w_scale_gu, const float* w_scale_d,
+                int E, int I, void* y, int act, int bm, int bn, char* ws, size_t ws_bytes,
+                flide_stream_t stream) {
+  if (!experts_args_ok(T, H, k, E, I, bm, x_dtype, act, w_scale_gu, w_scale_d)) return FLIDE_MOE_ERR_ARG;
+  if (T == 0) return FLIDE_MOE_OK;
+  const ExpertsLayout L = layout(T, k, E, H, I, bm, w_scale_gu != nullptr);
+  if (ws_bytes < L.total) return FLIDE_MOE_ERR_WORKSPACE;
+  int rc = flide_moe_align(ids, T * k, E, bm, (int*)(ws + L.rows), (int*)(ws + L.blocks), (int*)(ws + L.used),
+                           nullptr, ws + L.hist, L.rows - L.hist, stream);
+  if (rc) return rc;
+  return run_products(x, sx, x_dtype, T, H, top, k, w_gu, w_d, w_scale_gu, w_scale_d, E, I, y, act, bm, bn, ws,
+                      L, stream);
 }
 
 // The allocation-free entry point's scratch: one copy of this array per device, resident from module

@@ -9,7 +9,7 @@
 #include <float.h>
 #include <limits.h>
 
-#include "common.hpp"
+#include "routing.hpp"
 
 namespace {
 
@@ -290,69 +290,17 @@ __global__ __launch_bounds__(256) void gate_kernel(const u16* __restrict__ x, lo
   if (l == 0) gate[t] = s;
 }
 
-FLIDE_DEV float load_scalar(const void* p, int dtype, int i) {
-  if (dtype == FLIDE_F32) return ((const float*)p)[i];
-  if (dtype == FLIDE_BF16) return bf16_to_f32(((const u16*)p)[i]);
-  return f16_to_f32(((const u16*)p)[i]);
-}
-
 template <int EPL>
 __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ logits, long long sl,
                                                     int T_, int E, int k, const void* scale,
                                                     int scale_dtype, float* __restrict__ w,
                                                     int* __restrict__ ids) {
-  const int wave = threadIdx.x >> 6, l = threadIdx.x & 63;
-  const long long t = (long long)blockIdx.x * 4 + wave;
+  const long long t = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T_) return;
-  const float* row = logits + t * sl;
-  float v[EPL];
-#pragma unroll
-  for (int i = 0; i < EPL; ++i) {
-    int e = l + 64 * i;
-    v[i] = e < E ? row[e] : -INFINITY;
-  }
-  float m = v[0];
-#pragma unroll
-  for (int i = 1; i < EPL; ++i) m = fmaxf(m, v[i]);
-  m = wave_max(m);
-  float s = 0.f;
-#pragma unroll
-  for (int i = 0; i < EPL; ++i)
-    if (l + 64 * i < E) s += expf(v[i] - m);
-  s = wave_sum(s);
-  unsigned taken = 0;
-  float my_v = -INFINITY;   // lane j < k: the j-th selected logit and its id
-  int my_id = 0;
-  for (int j = 0; j < k; ++j) {
-    float bv = -INFINITY;
-    int bi = INT_MAX;
-#pragma unroll
-    for (int i = 0; i < EPL; ++i) {
-      int e = l + 64 * i;
-      bool free_ = e < E && !((taken >> i) & 1u);
-      // lanes hold ascending ids, so a strict > keeps the lower id among equal local values
-      if (free_ && (v[i] > bv || bi == INT_MAX)) {
-        bv = v[i];
-        bi = e;
-      }
-    }
-    wave_argmax(bv, bi);
-    if (bi != INT_MAX && (bi & 63) == l) taken |= 1u << (bi >> 6);
-    if (l == j) {
-      my_v = bv;
-      my_id = bi;
-    }
-  }
-  // probabilities of the selected experts, summed in slot order (lane reads of lanes 0..k-1)
-  const float my_p = l < k ? expf(my_v - m) / s : 0.f;
-  float topsum = 0.f;
-  for (int j = 0; j < k; ++j) topsum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_p), j));
-  if (l < k) {
-    float ww = my_p / topsum;
-    if (scale) ww *= load_scalar(scale, scale_dtype, my_id);
-    w[t * k + l] = ww;
-    ids[t * k + l] = my_id;
-  }
+  float v[EPL], sc[EPL];
+  routing::load_logits<EPL>(logits + t * sl, E, v);
+  routing::load_scales<EPL>(scale, scale_dtype, E, sc);
+  routing::route_select<EPL>(v, sc, E, k, w + t * k, ids + t * k, nullptr);
 }
 
 }  // namespace
