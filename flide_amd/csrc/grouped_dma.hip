@@ -23,75 +23,10 @@
 // Arithmetic is the same as every other grouped kernel here (common.hpp): 16-bit products in 32-wide
 // K steps with lane group g holding k = c*32 + g*8 + [0, 8); float8 in 128-wide steps with lane group g
 // holding k = g*16 + [0, 16) and 64 + g*16 + [0, 16).
-#include "grouped_common.hpp"
-
-#define FLIDE_GLOBAL_AS __attribute__((address_space(1)))
-#define FLIDE_LDS_AS __attribute__((address_space(3)))
+#include "dma_common.hpp"
 
 namespace {
 using namespace grouped_detail;
-
-__device__ __attribute__((aligned(16))) const uint32_t g_zero16[4] = {0, 0, 0, 0};
-
-template <int N> FLIDE_DEV void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-  // s_waitcnt: vmcnt[3:0] bits 3:0, vmcnt[5:4] bits 15:14; expcnt (6:4) and lgkmcnt (11:8) left open
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
-FLIDE_DEV void dma16(const void* src, FLIDE_LDS_AS void* dst) {
-  __builtin_amdgcn_global_load_lds((const FLIDE_GLOBAL_AS void*)src, dst, 16, 0, 0);
-}
-
-// The weight loads: non-temporal (`nt`, cache-policy bit 1 on gfx950) when NT, i.e. when every weight
-// byte is read by one block only (an expert's pairs fill one block). They then stop displacing the
-// activation rows that the block's column tiles share in L2: at 64 tokens gate/up streams 6.5 TB/s
-// instead of 5.7 (down 6.1 instead of 5.2); at 512-1024 tokens the bm-128 gate/up gains 4-6%. Where
-// several blocks share a weight tile (prefill) the same loads are 15-60% slower, so they stay plain.
-template <bool NT> FLIDE_DEV void dma16w(const void* src, FLIDE_LDS_AS void* dst) {
-  __builtin_amdgcn_global_load_lds((const FLIDE_GLOBAL_AS void*)src, dst, 16, 0, NT ? 2 : 0);
-}
-
-// chunk swizzle of a row with CPR 16-byte chunks (8 for 128-byte rows, 4 for 64-byte rows); both
-// measured bank-conflict-free for the fragment reads below
-template <int CPR> FLIDE_DEV int swz(int row) { return CPR == 8 ? (row & 7) : ((row >> 1) & 3); }
-
-// Waits until at most `ahead` (0 .. NS-2) stages of this wave's loads are still in flight (each stage =
-// L loads).
-template <int NS, int L> FLIDE_DEV void wait_stage(int ahead) {
-  static_assert(NS >= 2 && NS <= 4, "stage ring of 2..4");
-  if constexpr (NS >= 4) {
-    if (ahead >= 2) { wait_vmcnt<2 * L>(); return; }
-  }
-  if constexpr (NS >= 3) {
-    if (ahead >= 1) { wait_vmcnt<L>(); return; }
-  }
-  wait_vmcnt<0>();
-}
-
-// Element type traits of the two kernel families: 16-bit (2 bytes, 64 K per 128-byte stage row, two
-// 32-wide MFMA steps) and float8 (1 byte, 128 K per stage row, one 128-wide MFMA step).
-template <typename T> struct DmaElem {
-  static constexpr int BYTES = 2;
-};
-struct Fp8Tag {};
-template <> struct DmaElem<Fp8Tag> {
-  static constexpr int BYTES = 1;
-};
-
-// First block of the run of blocks holding expert e that contains block blk (blocks[blk] == e; align
-// writes each expert's blocks contiguously): the wave looks 64 entries back at a time until an entry
-// differs. Entries below blk are all in use, and a lane below 0 reads -1, so the loop ends.
-FLIDE_DEV int expert_first_block(const int* blocks, int blk, int e, int l) {
-  int base = blk;
-  for (;;) {
-    const int idx = base - 63 + l;
-    const int v = idx >= 0 ? blocks[idx] : -1;
-    const unsigned long long m = __ballot(v != e);
-    if (m) return base - 63 + (63 - __builtin_clzll(m)) + 1;
-    base -= 64;
-  }
-}
 
 template <typename T, typename OutT, int ACT, int BM, int BN, int WAVES_M, int WAVES_N, int NS, int ROWB, int OCC,
           int XCD_CHUNK_BLOCKS, bool NTW>
@@ -129,12 +64,13 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void grouped_dma(Group
   // Workgroup b runs on XCD b % 8.
   int pm, pn;
   if constexpr (BM >= 64) {
-    // Prefill tiles: the items (block, column tile) in use, ordered by expert, then block, then column
-    // tile, are split into 8 contiguous ranges, range x for the workgroups of XCD x. An expert's blocks
-    // and all its column tiles then run on one XCD at about the same time, so each weight tile comes
-    // from HBM once and is shared in that XCD's L2 (HBM fetch of the 16-bit gate/up product at 8192
-    // tokens: 3.1 -> 2.1-3.2 GB depending on the order inside an expert; this order measured fastest,
-    // 6-11% on the gate/up products at 4096-16384 tokens, no change on the down products).
+    // Prefill tiles: the items (block, column tile) in use, ordered by expert, are split into 8
+    // contiguous ranges, range x for the workgroups of XCD x. An expert's blocks and all its column
+    // tiles then run on one XCD at about the same time, so each weight tile comes from HBM about once
+    // and is shared in that XCD's L2. Inside an expert the gated (gate/up) products run column-tile
+    // major, so the expert's blocks load each weight tile together (HBM fetch of the 16-bit gate/up
+    // product at 8192 tokens 3.1 -> 2.1 GB; gate/up 4-11% faster at 4096-16384 tokens than the XCD
+    // chunks below); the plain (down) products run block major, measured 2-3% faster for them.
     const int nused = *p.used / BM;
     const long long R = (long long)nused * p.ntn;
     const int x = blockIdx.x & 7;
@@ -144,8 +80,14 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void grouped_dma(Group
     const int ex = p.blocks[blk];
     const int s0 = __builtin_amdgcn_readfirstlane(expert_first_block(p.blocks, blk, ex, l));
     const int local = (int)(it - (long long)s0 * p.ntn);
-    pm = s0 + local / p.ntn;
-    pn = local % p.ntn;
+    if constexpr (ACT != ACT_NONE) {
+      const int nb = __builtin_amdgcn_readfirstlane(expert_end_block(p.blocks, blk, ex, nused, l)) - s0;
+      pn = local / nb;
+      pm = s0 + local % nb;
+    } else {
+      pm = s0 + local / p.ntn;
+      pn = local % p.ntn;
+    }
   } else {
     // Decode tiles: items are cut into chunks of CH items (a few blocks of one expert and all their
     // column tiles) and chunk c goes to XCD c % 8, so each XCD's workgroups reuse the chunk's rows and
