@@ -6,6 +6,7 @@
                                          <copy_fetch.csv> <copy_write.csv> <command> > traffic.md
     python -m flide_amd.rocprof mfma <counters.csv> <kernel-regex> <flop-per-dispatch> <peak-flop/s> \\
                                       <title> <command> > mfma.md
+    python -m flide_amd.rocprof pipe <kernel-regex> <title> <command> <pass1.csv> [<pass2.csv> ...] > pipe.md
 
 `copy` runs a plain device-to-device copy of COPY_BYTES (the HIP runtime's copy kernel) a few times. Under
 `rocprofv3 --pmc FETCH_SIZE` and `--pmc WRITE_SIZE` its counters give the scale from the counters'
@@ -180,6 +181,55 @@ def mfma_md(path: str, regex: str, flop: float, peak: float, title: str, command
     return "\n".join(lines)
 
 
+PIPE_PASSES = (
+    "SQ_WAVE_CYCLES SQ_BUSY_CYCLES SQ_WAIT_ANY SQ_WAIT_INST_ANY SQ_WAIT_INST_LDS SQ_ACTIVE_INST_LDS "
+    "SQ_ACTIVE_INST_VALU SQ_INSTS_MFMA GRBM_GUI_ACTIVE",
+    "SQ_INSTS_VMEM SQ_INSTS_LDS SQ_LDS_IDX_ACTIVE SQ_LDS_BANK_CONFLICT SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE",
+    "TA_TA_BUSY TA_ADDR_STALLED_BY_TC_CYCLES TD_TD_BUSY TD_TC_STALL TCP_TCC_READ_REQ TCP_TCC_READ_REQ_LATENCY "
+    "TCP_PENDING_STALL_CYCLES TCP_TOTAL_CACHE_ACCESSES GRBM_GUI_ACTIVE",
+)
+CUS = 256
+
+
+def pipe_md(regex: str, title: str, command: str, paths: list[str]) -> str:
+    """Where a kernel's time goes along the memory pipe, medians over the dispatches matching `regex`,
+    from several --pmc passes of the same command. Unit-cycle counters are divided by the per-XCD
+    GRBM_GUI_ACTIVE and the 256 CUs (a fraction of CU cycles); TCP_TCC_READ_REQ_LATENCY, the cycles
+    L2 read requests spend outstanding, gives the average requests in flight per CU (Little's law) and,
+    over TCP_TCC_READ_REQ, the average L2 read latency."""
+    vals: dict[str, float] = {}
+    for path in paths:
+        ds = list(_dispatches(path, regex).values())
+        if not ds:
+            raise SystemExit(f"no dispatches matched {regex} in {path}")
+        for key in ds[0]:
+            vals.setdefault(key, statistics.median(d.get(key, 0.0) for d in ds))
+    gui = vals["GRBM_GUI_ACTIVE"] / XCDS
+    per_cu = lambda key: vals.get(key, 0.0) / CUS / gui   # noqa: E731
+    req, lat = vals.get("TCP_TCC_READ_REQ", 0.0), vals.get("TCP_TCC_READ_REQ_LATENCY", 0.0)
+    rows = [
+        ("duration (median, under counter collection)", f"{vals['ns'] / 1e3:.1f} us"),
+        ("shader clock", f"{gui / vals['ns']:.2f} GHz"),
+        ("MFMA busy (of SIMD cycles)", f"{vals.get('SQ_VALU_MFMA_BUSY_CYCLES', 0.0) / (gui * SIMDS):.1%}"),
+        ("TA busy (address unit, of CU cycles)", f"{per_cu('TA_TA_BUSY'):.1%}"),
+        ("TD busy (data return to VGPRs / LDS)", f"{per_cu('TD_TD_BUSY'):.1%}"),
+        ("TD stalled waiting on the L1/L2", f"{per_cu('TD_TC_STALL'):.1%}"),
+        ("L1 stalled on pending misses", f"{per_cu('TCP_PENDING_STALL_CYCLES'):.1%}"),
+        ("L1 -> L2 read requests per CU per cycle", f"{per_cu('TCP_TCC_READ_REQ'):.3f}"),
+        ("L2 read requests in flight per CU (average)", f"{per_cu('TCP_TCC_READ_REQ_LATENCY'):.1f}"),
+        ("average L2 read latency", f"{lat / req:.0f} cycles" if req else "-"),
+        ("L1 accesses per CU per cycle", f"{per_cu('TCP_TOTAL_CACHE_ACCESSES'):.3f}"),
+        ("LDS instructions / MFMA instructions", f"{vals.get('SQ_INSTS_LDS', 0.0) / max(vals.get('SQ_INSTS_MFMA', 1.0), 1.0):.2f}"),
+        ("LDS bank conflict cycles per CU per cycle", f"{per_cu('SQ_LDS_BANK_CONFLICT'):.3f}"),
+        ("global load instructions per CU per cycle", f"{per_cu('SQ_INSTS_VMEM'):.4f}"),
+    ]
+    lines = [f"# Memory pipe: {title}", "", f"Kernels matching `{regex}`; {len(paths)} rocprofv3 `--pmc` passes:", ""]
+    lines += ["```", command, "```", "", "| quantity | value |", "|---|---|"]
+    lines += [f"| {a} | {b} |" for a, b in rows]
+    lines.append("")
+    return "\n".join(lines)
+
+
 def traffic_for(workload: str, kernel: str = "gate_up") -> int | None:
     """The committed traffic figure of one product (`gate_up` or `down`) at a bench workload
     (profiles/<kernel>_<workload>_traffic.md), if any."""
@@ -203,6 +253,9 @@ def main(argv: list[str]) -> int:
         return 0
     if argv[0] == "traffic" and len(argv) == 8:
         print(traffic_md(*argv[1:]))
+        return 0
+    if argv[0] == "pipe" and len(argv) >= 5:
+        print(pipe_md(argv[1], argv[2], argv[3], argv[4:]))
         return 0
     if argv[0] == "mfma" and len(argv) == 7:
         print(mfma_md(argv[1], argv[2], float(argv[3]), float(argv[4]), argv[5], argv[6]))
