@@ -109,11 +109,15 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void grouped_dma(Group
     }
     if (pm >= p.nbm || pm * BM >= *p.used) return;
   }
-  const long long e = p.blocks[pm];
+  const long long e = __builtin_amdgcn_readfirstlane(p.blocks[pm]);
   const int K = p.K;
   const int half = p.N / 2;
   const char* A = (const char*)p.a;
   const char* B = (const char*)p.w + e * p.sbe * EB;
+  // full stages load through buffer resources over the activation rows and the expert's weight rows
+  const long long a_rows = p.by_token ? (p.n_pairs + p.topk - 1) / p.topk : p.n_pairs;
+  const __amdgpu_buffer_rsrc_t rsA = buf_rsrc(A, ((a_rows - 1) * p.sa + K) * EB);
+  const __amdgpu_buffer_rsrc_t rsB = buf_rsrc(B, ((long long)(p.N - 1) * p.sbn + K) * EB);
   const int kc = ((l % CPR) ^ swz<CPR>(l / CPR)) * (16 / EB);
   uint32_t b_off32[LB];
 #pragma unroll
@@ -141,7 +145,7 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void grouped_dma(Group
       FLIDE_LDS_AS char* sb = (FLIDE_LDS_AS char*)slots[st];
 #pragma unroll
       for (int i = 0; i < LB; ++i)
-        dma16w<NTW>(B + (long long)st * KS * EB + b_off32[i], sb + A_BYTES + (wave * LB + i) * 1024);
+        dma16b<NTW ? 2 : 0>(rsB, b_off32[i], (uint32_t)(st * KS * EB), sb + A_BYTES + (wave * LB + i) * 1024);
     }
   }
   for (int r = tid; r < BM; r += NW * 64) {
@@ -158,8 +162,8 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void grouped_dma(Group
   // c = (l % CPR) ^ swz(row). Instruction rows start at multiples of RPI, so swz(row) and therefore c
   // (and the chunk's K offset kc) depend on the lane only.
   // Per-lane 32-bit byte offsets from the operands' uniform bases (A rows are gathered pairs, B rows
-  // the expert's weight rows); a stage adds its uniform K offset to the base, so a full stage's load is
-  // base (SGPRs) + offset (one VGPR). Both tensors stay below 4 GB.
+  // the expert's weight rows); a full stage's load is buffer resource (SGPRs) + offset (one VGPR) +
+  // the stage's K offset (one SGPR). Both tensors stay below 4 GB.
   uint32_t a_off32[LA];
 #pragma unroll
   for (int i = 0; i < LA; ++i) {
@@ -219,13 +223,11 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void grouped_dma(Group
     // loads of a full stage kt (k0 + KS <= K) into ring slot `slot`: uniform base + lane offset
     auto issue = [&](int kt, int slot) {
       FLIDE_LDS_AS char* sb = (FLIDE_LDS_AS char*)slot_ptr(slot);
-      const long long kb = (long long)kt * KS * EB;
-      const char* Ak = A + kb;
-      const char* Bk = B + kb;
+      const uint32_t kb = (uint32_t)(kt * KS * EB);
 #pragma unroll
-      for (int i = 0; i < LA; ++i) dma16(Ak + a_off32[i], sb + (wave * LA + i) * 1024);
+      for (int i = 0; i < LA; ++i) dma16b<0>(rsA, a_off32[i], kb, sb + (wave * LA + i) * 1024);
 #pragma unroll
-      for (int i = 0; i < LB; ++i) dma16w<NTW>(Bk + b_off32[i], sb + A_BYTES + (wave * LB + i) * 1024);
+      for (int i = 0; i < LB; ++i) dma16b<NTW ? 2 : 0>(rsB, b_off32[i], kb, sb + A_BYTES + (wave * LB + i) * 1024);
     };
     // the partial last stage (K % KS != 0): chunks past K read a 16-byte block of zeros
     auto issue_tail = [&](int kt, int slot) {
@@ -286,7 +288,7 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void grouped_dma(Group
     for (int st = 0; st < NS - 1; ++st) {   // activation parts; the weight parts are in flight already
       FLIDE_LDS_AS char* sb = (FLIDE_LDS_AS char*)slot_ptr(st);
 #pragma unroll
-      for (int i = 0; i < LA; ++i) dma16(A + (long long)st * KS * EB + a_off32[i], sb + (wave * LA + i) * 1024);
+      for (int i = 0; i < LA; ++i) dma16b<0>(rsA, a_off32[i], (uint32_t)(st * KS * EB), sb + (wave * LA + i) * 1024);
     }
     wait_vmcnt<0>();
     // steady state: stage kt computes while stages kt+1 .. kt+NS-1 load; every stage it issues is full
@@ -376,29 +378,35 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void grouped_dma(Group
 }
 
 // Float8 plain (down) products with short rows (K <= 768, the 704-wide down product): the block's
-// activation rows stay resident in LDS and one loader wave streams the expert's weight tiles through a
+// activation rows stay resident in LDS and NLD loader waves stream the expert's weight tiles through a
 // ring, continuously over several column tiles. With K this short, the per-tile kernel above spends
 // most of a block's life filling and draining its ring (6 stages per tile); here the ring runs across
 // tile boundaries and the activation rows are read once per block, not once per tile.
 //
 // Roles: waves 0-7 (2 x 4, each 64 rows x 32 columns of a 128 x 128 tile) load the activation rows
-// once, then only read LDS, issue MFMAs and store; wave 8 only issues direct-to-LDS weight loads and
-// waits for them. A wave's vmcnt counts its own memory operations, so the compute waves' epilogue
-// stores never hold up the loads' waits (in a single-role kernel every wait after a store would wait
-// for that store too). One barrier per stage: at stage s the loader has waited for stage s and the
-// compute waves have finished stage s - 1, whose ring slot the loader refills right after it.
-// The column scales of tile t travel with every stage of tile t (BN / 64 loads of 256 bytes, so every
-// stage holds the same number of loads) into s_ws[t & 1], read by the tile's epilogue.
+// once, then only read LDS, issue MFMAs and store; waves 8 .. 8 + NLD - 1 only issue direct-to-LDS
+// weight loads and wait for them. A wave's vmcnt counts its own memory operations, so the compute
+// waves' epilogue stores never hold up the loads' waits (in a single-role kernel every wait after a
+// store would wait for that store too). One barrier per stage: at stage s the loaders have waited for
+// stage s and the compute waves have finished stage s - 1, whose ring slot the loaders refill right
+// after it. Each loader issues 1 / NLD of a stage's weight rows: one wave issuing them all measured
+// as the bound of this kernel (the float8 down product at 4096 tokens 247 us with one loader wave,
+// 204 with two, 190 with four; eight need more waves per SIMD than the compute waves' registers allow).
+// The column scales of tile t travel with every stage of tile t (BN / 64 loads of 256 bytes, issued by
+// loaders 0 .. BN / 64 - 1, so each loader's stages hold the same number of loads) into s_ws[t & 1],
+// read by the tile's epilogue.
 //
 // Arithmetic: the same 128-wide K steps, lane mapping, MFMA and epilogue order as grouped_dma, so the
 // output bits are the same.
-template <typename OutT, int NS, int BN, int KT_MAX, int XB>
-__global__ __launch_bounds__(9 * 64, 1) void grouped_fp8_resident(GroupArgs p, int tpb, int nch) {
+template <typename OutT, int NS, int BN, int KT_MAX, int XB, int NLD>
+__global__ __launch_bounds__((8 + NLD) * 64, 1) void grouped_fp8_resident(GroupArgs p, int tpb, int nch) {
   constexpr int BM = 128, ROWB = 128;
   constexpr int WAVES_M = 2, WM = 64, WN = BN / 4, FM = 4, FN = WN / 16;
   constexpr int A_KT = BM * ROWB, B_BYTES = BN * ROWB;
-  constexpr int LB = BN / 8, LW = BN / 64, LPS = LB + LW;   // loads per stage: weight rows, scales
-  static_assert((NS - 1) * LPS < 64 && 2 * KT_MAX < 64, "loads in flight must fit vmcnt");
+  constexpr int LB = BN / 8, LW = BN / 64;   // loads per stage: weight rows, scales
+  constexpr int LBW = LB / NLD;               // weight loads per loader wave and stage
+  static_assert(LB % NLD == 0 && (NLD == 1 || LW <= NLD), "loaders split the stage evenly");
+  static_assert((NS - 1) * (LBW + LW) < 64 && 2 * KT_MAX < 64, "loads in flight must fit vmcnt");
   static_assert(NS >= 3 && NS <= 6 && BN % 64 == 0 && FN >= 1, "ring of 3..6 slots, 64-row multiples");
 
   __shared__ __attribute__((aligned(1024))) char s_a[KT_MAX * A_KT];
@@ -423,7 +431,7 @@ __global__ __launch_bounds__(9 * 64, 1) void grouped_fp8_resident(GroupArgs p, i
   const int K = p.K, KT = (K + ROWB - 1) / ROWB;
   const int S = nt * KT;
   const long long e = p.blocks[pm];
-  for (int r = tid; r < BM; r += 9 * 64) {
+  for (int r = tid; r < BM; r += (8 + NLD) * 64) {
     const int pair = p.rows[pm * BM + r];
     s_pairs[r] = pair;
     const bool ok = pair < p.n_pairs;
@@ -436,7 +444,8 @@ __global__ __launch_bounds__(9 * 64, 1) void grouped_fp8_resident(GroupArgs p, i
   // (l % 8) ^ (row & 7); rows start at multiples of 8, so the chunk's byte offset depends on l only
   const int kc = ((l & 7) ^ (l >> 3)) * 16;
 
-  if (wave == 8) {   // ---------------- loader ----------------
+  if (wave >= 8) {   // ---------------- loaders ----------------
+    const int li = wave - 8;
     const char* B = (const char*)p.w + e * p.sbe;
     const float* WS = p.w_scale + e * p.sse;
     auto issue = [&](int s) {
@@ -445,29 +454,36 @@ __global__ __launch_bounds__(9 * 64, 1) void grouped_fp8_resident(GroupArgs p, i
       const int k0 = kt * ROWB;
       const bool in = k0 + kc < K;
 #pragma unroll
-      for (int i = 0; i < LB; ++i) {
-        const int n = min(t * BN + i * 8 + (l >> 3), p.N - 1);
-        dma16(in ? (const void*)(B + (long long)n * p.sbn + k0 + kc) : (const void*)g_zero16, sb + i * 1024);
+      for (int i = 0; i < LBW; ++i) {   // rows (li * LBW + i) * 8 .. + 7 of the tile
+        const int ii = li * LBW + i;
+        const int n = min(t * BN + ii * 8 + (l >> 3), p.N - 1);
+        dma16(in ? (const void*)(B + (long long)n * p.sbn + k0 + kc) : (const void*)g_zero16, sb + ii * 1024);
       }
-#pragma unroll
-      for (int i = 0; i < LW; ++i) {
-        const int col = min(t * BN + i * 64 + l, p.N - 1);
+      for (int q = li; q < LW; q += NLD) {
+        const int col = min(t * BN + q * 64 + l, p.N - 1);
         __builtin_amdgcn_global_load_lds((const FLIDE_GLOBAL_AS void*)(WS + col),
-                                         (FLIDE_LDS_AS void*)&s_ws[t & 1][i * 64], 4, 0, 0);
+                                         (FLIDE_LDS_AS void*)&s_ws[t & 1][q * 64], 4, 0, 0);
       }
     };
-    for (int s = 0; s < NS - 1 && s < S; ++s) issue(s);
-    for (int s = 0; s < S; ++s) {
-      const int ahead = min(NS - 2, S - 1 - s);   // stages after s already in flight
-      if (NS > 5 && ahead >= 4) wait_vmcnt<(NS > 5 ? 4 : 0) * LPS>();
-      else if (NS > 4 && ahead >= 3) wait_vmcnt<(NS > 4 ? 3 : 0) * LPS>();
-      else if (NS > 3 && ahead >= 2) wait_vmcnt<(NS > 3 ? 2 : 0) * LPS>();
-      else if (ahead >= 1) wait_vmcnt<LPS>();
-      else wait_vmcnt<0>();
-      __builtin_amdgcn_s_barrier();
-      asm volatile("" ::: "memory");
-      if (s + NS - 1 < S) issue(s + NS - 1);
-    }
+    // LPS: this loader's loads per stage (its weight rows, plus a scale load for loaders below LW)
+    auto loop = [&](auto lps_tag) {
+      constexpr int LPS = decltype(lps_tag)::value;
+      for (int s = 0; s < NS - 1 && s < S; ++s) issue(s);
+      for (int s = 0; s < S; ++s) {
+        const int ahead = min(NS - 2, S - 1 - s);   // stages after s already in flight
+        if (NS > 5 && ahead >= 4) wait_vmcnt<(NS > 5 ? 4 : 0) * LPS>();
+        else if (NS > 4 && ahead >= 3) wait_vmcnt<(NS > 4 ? 3 : 0) * LPS>();
+        else if (NS > 3 && ahead >= 2) wait_vmcnt<(NS > 3 ? 2 : 0) * LPS>();
+        else if (ahead >= 1) wait_vmcnt<LPS>();
+        else wait_vmcnt<0>();
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if (s + NS - 1 < S) issue(s + NS - 1);
+      }
+    };
+    if constexpr (NLD == 1) loop(std::integral_constant<int, LBW + LW>{});
+    else if (li < LW) loop(std::integral_constant<int, LBW + 1>{});
+    else loop(std::integral_constant<int, LBW>{});
     return;
   }
 
@@ -582,7 +598,7 @@ __global__ __launch_bounds__(9 * 64, 1) void grouped_fp8_resident(GroupArgs p, i
 // grouped_fp8_resident for a float8 plain product with 128-row blocks: K of 129..768 (whole 16-byte
 // chunks). Column tiles are split into chunks so that the grid holds at least about 640 items
 // (2.5 per CU at one workgroup per CU); returns FLIDE_MOE_ERR_TILE when the shape does not fit.
-template <typename OutT, int NS = 3, int BN = 128>
+template <typename OutT, int NS = 3, int BN = 128, int NLD = 4>
 int launch_fp8_resident(GroupArgs& p, hipStream_t st) {
   constexpr int KT_MAX = 6, XB = 4;
   // s_ws[t & 1] is refilled for tile t + 2 from stage (t + 2) * KT - (NS - 1) on, which must come after
@@ -596,8 +612,8 @@ int launch_fp8_resident(GroupArgs& p, hipStream_t st) {
   p.ntn = ntn;
   const int items = p.nbm * nch;
   const int round = 8 * nch * XB;
-  dim3 grid((items + round - 1) / round * round), block(9 * 64);
-  grouped_fp8_resident<OutT, NS, BN, KT_MAX, XB><<<grid, block, 0, st>>>(p, tpb, nch);
+  dim3 grid((items + round - 1) / round * round), block((8 + NLD) * 64);
+  grouped_fp8_resident<OutT, NS, BN, KT_MAX, XB, NLD><<<grid, block, 0, st>>>(p, tpb, nch);
   return FLIDE_MOE_OK;
 }
 
@@ -614,7 +630,8 @@ int launch_fp8_resident(GroupArgs& p, hipStream_t st) {
 //     and 3-7% (down) faster than 1 x 4 waves with 64-byte rows
 //  float8 (128-byte stage rows, one 128-wide MFMA step): bm 64 with BN = 128 and 2 stages (48 KB, three
 //     workgroups per CU); bm 128 in 8-wave workgroups: the plain (down) product 64 x 32 per wave, 2
-//     stages (375 -> 290 us at 4096 tokens; with K <= 768 grouped_fp8_resident replaces it, 251 us), the gated (gate/up) product 64 x 64 per wave with BN = 256
+//     stages (375 -> 290 us at 4096 tokens; with K <= 768 grouped_fp8_resident replaces it, 190 us),
+//     the gated (gate/up) product 64 x 64 per wave with BN = 256
 //     and 3 stages (144 KB; 5-10% faster than 2 x 2 waves of BN 128 at 4096-16384 tokens); bm 256:
 //     2 stages = 128 KB
 //  bm 32 (decode): 128-byte stage rows, 3 stages. 16-bit: BN = 64 (gated 2 x 2 waves, plain 1 x 4),
@@ -637,7 +654,7 @@ int launch_one(GroupArgs& p, hipStream_t st) {
   // XCD's range of the items in use is at most that long)
   const int round = BM >= 64 ? 8 : 8 * p.ntn * XB;
   dim3 grid((items + round - 1) / round * round), block(WM_ * WN_ * 64);
-  // Non-temporal weight loads (dma16w) for every 32-row (decode) product and for the gated products of
+  // Non-temporal weight loads (dma16w / dma16b<2>) for every 32-row (decode) product and for the gated products of
   // larger tiles while padding fills at least half the blocks (most experts then hold one block, so each
   // weight tile is read once); the plain (down) products of larger tiles measured slower with them. Only
   // for weight rows of whole 128-byte lines: a row that ends mid-line (float8 down rows of 704 bytes)
