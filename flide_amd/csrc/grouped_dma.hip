@@ -58,6 +58,7 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void grouped_dma(Group
   __shared__ __attribute__((aligned(1024))) char lds3[NS > 3 ? STAGE : 16];
   __shared__ int s_pairs[BM];
   __shared__ float s_ascale[FP8 ? BM : 1];
+  __shared__ float s_wt[ACT == ACT_NONE ? BM : 1];   // plain products: the rows' routing weights
 
   const int tid = threadIdx.x, l = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform, in an SGPR
@@ -155,6 +156,7 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void grouped_dma(Group
       const long long src = p.by_token ? pair / p.topk : pair;
       s_ascale[r] = pair < p.n_pairs ? p.a_scale[src] : 0.f;
     }
+    if constexpr (ACT == ACT_NONE) s_wt[r] = p.weights && pair < p.n_pairs ? p.weights[pair] : 1.f;
   }
   __syncthreads();
 
@@ -356,13 +358,24 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void grouped_dma(Group
     float rs[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) rs[i] = FP8 ? s_ascale[row0 + g * 4 + i] : 1.f;
-    if constexpr (ACT == ACT_NONE) {
+    if constexpr (ACT == ACT_NONE && !FP8 && std::is_same<OutT, float>::value) {
+      if (p.pack_f32) {
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn) store_frag_f32x4(p, s_pairs, s_wt, row0, colbase[fn], acc[fm][fn], rs, 1.f);
+      } else {
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn) {
+          const int col = colbase[fn] + r;
+          store_frag<OutT, ACT, RT>(p, s_pairs, row0, col, acc[fm][fn], acc[fm][fn], 1.f, 1.f, rs, col < p.N, s_wt);
+        }
+      }
+    } else if constexpr (ACT == ACT_NONE) {
 #pragma unroll
       for (int fn = 0; fn < FN; ++fn) {
         const int col = colbase[fn] + r;
         const bool ok = col < p.N;
         store_frag<OutT, ACT, RT>(p, s_pairs, row0, col, acc[fm][fn], acc[fm][fn],
-                                  FP8 ? (ok ? ws[col] : 0.f) : 1.f, 1.f, rs, ok);
+                                  FP8 ? (ok ? ws[col] : 0.f) : 1.f, 1.f, rs, ok, s_wt);
       }
     } else {
 #pragma unroll
@@ -650,6 +663,7 @@ int launch_one(GroupArgs& p, hipStream_t st) {
   const int per = ACT == ACT_NONE ? BN : BN / 2;
   p.ntn = (cols + per - 1) / per;
   const int items = p.nbm * p.ntn;
+  p.pack_f32 = std::is_same<OutT, float>::value && p.sc % 4 == 0 && (uintptr_t)p.out % 16 == 0;
   // decode tiles: whole XCD chunks; prefill tiles: eight equal ranges of the static item count (each
   // XCD's range of the items in use is at most that long)
   const int round = BM >= 64 ? 8 : 8 * p.ntn * XB;
