@@ -50,6 +50,16 @@ template <bool NT> FLIDE_DEV void dma16w(const void* src, FLIDE_LDS_AS void* dst
 // measured bank-conflict-free for the fragment reads below
 template <int CPR> FLIDE_DEV int swz(int row) { return CPR == 8 ? (row & 7) : ((row >> 1) & 3); }
 
+// The barrier of a stage ring, taken by every wave that reads the ring: its own LDS reads complete
+// first. gfx950's s_barrier does not wait for outstanding memory operations, and the compiler leaves
+// reads of the slot consumed last in flight across it (the MFMAs that use them follow the barrier),
+// while the loads issued right after the barrier refill that very slot: without the wait, another
+// wave's direct-to-LDS write could land before such a read is served.
+FLIDE_DEV void ring_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0); vmcnt (bits 3:0, 15:14) and expcnt (6:4) open
+  __builtin_amdgcn_s_barrier();
+}
+
 // Waits until at most `ahead` (0 .. NS-2) stages of this wave's loads are still in flight (each stage =
 // L loads).
 template <int NS, int L> FLIDE_DEV void wait_stage(int ahead) {

@@ -300,7 +300,7 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void grouped_dma(Group
 #pragma unroll
       for (int slot = 0; slot < NS; ++slot) {
         wait_stage<NS, L>(NS - 2);
-        __builtin_amdgcn_s_barrier();
+        ring_barrier();
         issue(kt0 + slot + NS - 1, (slot + NS - 1) % NS);
         compute(slot);
       }
@@ -312,7 +312,7 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void grouped_dma(Group
       const int kt = kt0 + i;
       if (kt < nk) {
         wait_stage<NS, L>(min(NS - 2, nk - 1 - kt));
-        __builtin_amdgcn_s_barrier();
+        ring_barrier();
         const int ks = kt + NS - 1;
         if (ks < nfull) issue(ks, (i + NS - 1) % NS);
         else if (ks < nk) issue_tail(ks, (i + NS - 1) % NS);
@@ -552,7 +552,7 @@ __global__ __launch_bounds__((8 + NLD) * 64, 1) void grouped_fp8_resident(GroupA
     const bool mulw = p.weights != nullptr;
     int kt = 0, slot = 0, t = t0;
     for (int s = 0; s < S; ++s) {
-      __builtin_amdgcn_s_barrier();
+      ring_barrier();
       asm volatile("" ::: "memory");
       if constexpr (FMA > 0) {
         const char* sa_ = s_a + kt * A_KT + wm * WM * ROWB;
