@@ -143,6 +143,37 @@ def test_grouped_bf16(bm, by_token, mul_w, out32, dt):
     assert_close(np32(out), ref, REL_BF16 if not out32 else 1e-5, "grouped")
 
 
+@pytest.mark.parametrize("bm", [32, 64, 128])
+@pytest.mark.parametrize("layout", ["tail", "strided"])
+@pytest.mark.parametrize("mul_w", [True, False])
+def test_grouped_f32_out_layouts(bm, layout, mul_w):
+    """Float32 outputs of the plain product in the layouts its epilogue treats differently: 4 columns
+    per lane when out and its row stride are 4-float aligned (here with N % 4 != 0, so the last group of
+    each row is partial), one column per lane otherwise (a view one float into a row of stride 203).
+    Columns outside the view stay untouched."""
+    print(f"grouped f32 out bm={bm} {layout} mul_w={mul_w}", flush=True)
+    moe = _moe()
+    g = torch.Generator().manual_seed(300 + bm)
+    T, E, k, K = 80, 10, 3, 200
+    N, width, c0 = (202, 204, 0) if layout == "tail" else (200, 203, 1)
+    logits = torch.randn(T, E, generator=g)
+    _, ids = orc.route(logits.numpy(), k)
+    a = torch.randn(T, K, generator=g).to(torch.bfloat16)
+    w = (torch.randn(E, N, K, generator=g) * 0.05).to(torch.bfloat16)
+    wts = torch.rand(T * k, generator=g)
+    rows, blocks, used = moe.align(torch.from_numpy(ids).to(DEV), E, bm)
+    buf = torch.full((T * k, width), float("nan"), device=DEV, dtype=torch.float32)
+    out = buf[:, c0:c0 + N]
+    moe.grouped(a.to(DEV), w.to(DEV), out, rows, blocks, used, k, True, wts.to(DEV) if mul_w else None,
+                tile=(bm, 128, 4, 2))
+    al = orc.align(ids, E, bm)
+    ref = orc.grouped(np32(a), np32(w), al["rows"], al["blocks"], al["used"], T * k, k, True,
+                      wts.numpy() if mul_w else None, bm=bm, out_dtype="fp32")
+    assert_close(np32(out), ref, 1e-5, f"f32 out {layout}")
+    rest = torch.cat([buf[:, :c0], buf[:, c0 + N:]], 1)
+    assert torch.isnan(rest).all(), "a store landed outside the output view"
+
+
 @pytest.mark.parametrize("bm", [16, 32, 64, 128, 256])
 @pytest.mark.parametrize("act", ["geglu", "swiglu"])
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
