@@ -159,15 +159,18 @@ __global__ __launch_bounds__(RW_THREADS) void combine_norm_bf16_kernel(const YT*
     for (int j = 0; j < KMAX; ++j) {
       if (j >= k) break;
       const long long row = (t * k + j) * (long long)H;
-      // y is read exactly once: non-temporal loads keep it from evicting what the other wavefronts'
-      // rows still need (combine_norm at 8192 tokens: 153 -> 134 us, 6.2 TB/s)
+      // y is read exactly once: float32 rows with non-temporal loads, which keep them from evicting
+      // what the other wavefronts' rows still need (combine_norm at 8192 tokens: 153 -> 134 us,
+      // 6.2 TB/s); 16-bit rows (8 bytes per lane) with plain loads, faster for them when y comes
+      // from HBM (4096 tokens, bf16 y: 53 -> 40 us; no difference right after the down product,
+      // whose y the next read finds mostly in the last-level cache)
       if constexpr (std::is_same<YT, float>::value) {
         typedef float f32x4v __attribute__((ext_vector_type(4)));
         const f32x4v t = __builtin_nontemporal_load((const f32x4v*)(y + row) + c4);
         yv[j] = make_float4(t[0], t[1], t[2], t[3]);
       } else {
         typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
-        const u32x2v raw = __builtin_nontemporal_load((const u32x2v*)(y + row) + c4);
+        const u32x2v raw = *((const u32x2v*)(y + row) + c4);
         yv[j] = make_float4(bf16_to_f32(raw[0] & 0xffff), bf16_to_f32(raw[0] >> 16), bf16_to_f32(raw[1] & 0xffff),
                             bf16_to_f32(raw[1] >> 16));
       }
@@ -282,7 +285,7 @@ __global__ __launch_bounds__(RW_THREADS) void combine_vec_kernel(const YT* __res
         yv[j] = make_float4(q[0], q[1], q[2], q[3]);
       } else {
         typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
-        const u32x2v raw = __builtin_nontemporal_load((const u32x2v*)(y + row) + c4);
+        const u32x2v raw = *((const u32x2v*)(y + row) + c4);   // 16-bit rows: plain loads (as combine_norm)
         yv[j] = make_float4(bf16_to_f32(raw[0] & 0xffff), bf16_to_f32(raw[0] >> 16), bf16_to_f32(raw[1] & 0xffff),
                             bf16_to_f32(raw[1] >> 16));
       }
