@@ -411,10 +411,12 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void grouped_dma(Group
 //
 // Arithmetic: the same 128-wide K steps, lane mapping, MFMA and epilogue order as grouped_dma, so the
 // output bits are the same.
-template <typename OutT, int NS, int BN, int KT_MAX, int XB, int NLD>
+template <typename OutT, int NS, int BN, int KT_MAX, int XB, int NLD, bool WIDE>
 __global__ __launch_bounds__((8 + NLD) * 64, 1) void grouped_fp8_resident(GroupArgs p, int tpb, int nch) {
   constexpr int BM = 128, ROWB = 128;
-  constexpr int WAVES_M = 2, WM = 64, WN = BN / 4, FM = 4, FN = WN / 16;
+  // compute waves: WIDE (16-bit outputs, aligned): 8 x 1 waves of 16 rows x BN columns, each wave owning
+  // whole output row segments of the tile; else 2 x 4 waves of 64 x BN / 4
+  constexpr int WAVES_M = WIDE ? 8 : 2, WM = BM / WAVES_M, WN = BN / (8 / WAVES_M), FM = WM / 16, FN = WN / 16;
   constexpr int A_KT = BM * ROWB, B_BYTES = BN * ROWB;
   constexpr int LB = BN / 8, LW = BN / 64;   // loads per stage: weight rows, scales
   constexpr int LBW = LB / NLD;               // weight loads per loader wave and stage
@@ -428,6 +430,8 @@ __global__ __launch_bounds__((8 + NLD) * 64, 1) void grouped_fp8_resident(GroupA
   __shared__ int s_pairs[BM];
   __shared__ float s_ascale[BM];
   __shared__ float s_wt[BM];
+  // WIDE epilogue: each wave turns 4 output rows at a time into row-major 16-bit values here
+  __shared__ __attribute__((aligned(16))) uint16_t s_stage[WIDE ? 8 : 1][WIDE ? 4 * BN : 8];
 
   const int tid = threadIdx.x, l = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -574,7 +578,41 @@ __global__ __launch_bounds__((8 + NLD) * 64, 1) void grouped_fp8_resident(GroupA
         for (int fm = 0; fm < FMA; ++fm)
 #pragma unroll
           for (int fn = 0; fn < FN; ++fn) acc[fm][fn] = mfma_fp8(af[fm], bfr[fn], acc[fm][fn]);
-        if (kt == KT - 1) {   // epilogue of tile t: out = acc * s_a[row] * s_w[col] (* routing weight)
+        if (WIDE && kt == KT - 1) {   // epilogue of tile t, 4 rows at a time through LDS (see the launcher)
+          float cs[FN];
+#pragma unroll
+          for (int fn = 0; fn < FN; ++fn) cs[fn] = s_ws[t & 1][wn * WN + fn * 16 + r];
+          uint16_t* stg = s_stage[wave];
+          const int c8 = (l & 15) * 8;   // this lane's 8 columns of the staged row l / 16 (= g)
+          const int col0 = t * BN + c8;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {   // output register i: rows g * 4 + i (one per lane group g)
+#pragma unroll
+            for (int fn = 0; fn < FN; ++fn) {
+              float v = acc[0][fn][i] * rsc[0][i] * cs[fn];
+              if (mulw) v *= rwt[0][i];
+              stg[g * BN + fn * 16 + r] = OutTraits<OutT>::conv(v);
+            }
+            __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): the wave's staging writes are done
+            const uint4 q = *(const uint4*)(stg + g * BN + c8);
+            const int pair = prow[0][i];
+            if (pair < p.n_pairs && col0 < p.N) {
+              uint16_t* o = (uint16_t*)p.out + (long long)pair * p.sc + col0;
+              if (col0 + 8 <= p.N) {
+                *(uint4*)o = q;
+              } else {
+                const uint16_t e[8] = {(uint16_t)(q.x & 0xffff), (uint16_t)(q.x >> 16), (uint16_t)(q.y & 0xffff),
+                                       (uint16_t)(q.y >> 16), (uint16_t)(q.z & 0xffff), (uint16_t)(q.z >> 16),
+                                       (uint16_t)(q.w & 0xffff), (uint16_t)(q.w >> 16)};
+#pragma unroll
+                for (int j = 0; j < 7; ++j)
+                  if (col0 + j < p.N) o[j] = e[j];
+              }
+            }
+          }
+#pragma unroll
+          for (int fn = 0; fn < FN; ++fn) acc[0][fn] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        } else if (!WIDE && kt == KT - 1) {   // epilogue of tile t: out = acc * s_a[row] * s_w[col] (* routing weight)
           float cs[FN];
 #pragma unroll
           for (int fn = 0; fn < FN; ++fn) cs[fn] = s_ws[t & 1][wn * WN + fn * 16 + r];
@@ -601,11 +639,16 @@ __global__ __launch_bounds__((8 + NLD) * 64, 1) void grouped_fp8_resident(GroupA
       if (++kt == KT) { kt = 0; ++t; }
     }
   };
-  if (nlive == 0) run(std::integral_constant<int, 0>{});
-  else if (nlive == 1) run(std::integral_constant<int, 1>{});
-  else if (nlive == 2) run(std::integral_constant<int, 2>{});
-  else if (nlive == 3) run(std::integral_constant<int, 3>{});
-  else run(std::integral_constant<int, 4>{});
+  if constexpr (FM == 1) {
+    if (nlive == 0) run(std::integral_constant<int, 0>{});
+    else run(std::integral_constant<int, 1>{});
+  } else {
+    if (nlive == 0) run(std::integral_constant<int, 0>{});
+    else if (nlive == 1) run(std::integral_constant<int, 1>{});
+    else if (nlive == 2) run(std::integral_constant<int, 2>{});
+    else if (nlive == 3) run(std::integral_constant<int, 3>{});
+    else run(std::integral_constant<int, 4>{});
+  }
 }
 
 // grouped_fp8_resident for a float8 plain product with 128-row blocks: K of 129..768 (whole 16-byte
@@ -626,7 +669,16 @@ int launch_fp8_resident(GroupArgs& p, hipStream_t st) {
   const int items = p.nbm * nch;
   const int round = 8 * nch * XB;
   dim3 grid((items + round - 1) / round * round), block((8 + NLD) * 64);
-  grouped_fp8_resident<OutT, NS, BN, KT_MAX, XB, NLD><<<grid, block, 0, st>>>(p, tpb, nch);
+  // 16-bit outputs whose rows take 16-byte stores: the WIDE layout, where each store instruction writes
+  // 4 rows x 256 bytes (whole lines) instead of 64 scattered 2-byte values
+  typedef typename OutTraits<OutT>::storage S;
+  if constexpr (sizeof(S) == 2) {
+    if (p.sc % 8 == 0 && (uintptr_t)p.out % 16 == 0) {
+      grouped_fp8_resident<OutT, NS, BN, KT_MAX, XB, NLD, true><<<grid, block, 0, st>>>(p, tpb, nch);
+      return FLIDE_MOE_OK;
+    }
+  }
+  grouped_fp8_resident<OutT, NS, BN, KT_MAX, XB, NLD, false><<<grid, block, 0, st>>>(p, tpb, nch);
   return FLIDE_MOE_OK;
 }
 

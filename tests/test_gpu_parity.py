@@ -297,6 +297,38 @@ def test_grouped_fp8_plain_bm128(T, E, k, N, K, odt, mul_w, by_token):
     assert_close(np32(out), ref, REL_BF16 if odt != torch.float32 else 1e-4, "fp8 plain bm128")
 
 
+@pytest.mark.parametrize("layout", ["tail", "offset"])
+def test_grouped_fp8_plain_out_views(layout):
+    """16-bit outputs of the FP8 plain product at bm 128 in the two layouts its epilogue treats
+    differently: rows of 8-element-aligned stride staged and stored 8 columns per lane, here with
+    N % 8 != 0 so the last group is partial ("tail"); and a view one element into the row, which takes
+    the per-column stores ("offset"). Columns outside the view stay untouched."""
+    print(f"grouped fp8 plain out view {layout}", flush=True)
+    moe = _moe()
+    T, E, k, K = 900, 12, 4, 704
+    N, width, c0 = (700, 704, 0) if layout == "tail" else (512, 520, 1)
+    g = torch.Generator().manual_seed(N + c0)
+    _, ids = orc.route(torch.randn(T, E, generator=g).numpy(), k)
+    x = torch.randn(T * k, K, generator=g).to(torch.bfloat16)
+    w = (torch.randn(E, N, K, generator=g) * 0.05).to(torch.bfloat16)
+    wts = torch.rand(T * k, generator=g)
+    rows, blocks, used = moe.align(torch.from_numpy(ids).to(DEV), E, 128)
+    buf = torch.full((T * k, width), float("nan"), device=DEV, dtype=torch.bfloat16)
+    out = buf[:, c0:c0 + N]
+    qw, sw = orc.quantize_experts(np32(w))
+    qx, sx = orc.quantize_tokens(np32(x))
+    wq = torch.from_numpy(orc.e4m3fn_encode(qw)).view(torch.float8_e4m3fn).to(DEV)
+    moe.grouped_fp8(x.to(DEV), wq, torch.from_numpy(sw).to(DEV), out, rows, blocks, used, k, False,
+                    wts.to(DEV), tile=(128, 128, 4, 2))
+    al = orc.align(ids, E, 128)
+    ref = orc.grouped(qx * sx, qw * sw[:, :, None], al["rows"], al["blocks"], al["used"], T * k, k, False,
+                      wts.numpy(), bm=128, out_dtype="bf16")
+    assert not np.isnan(np32(out)).any(), "a valid pair's row was not written"
+    assert_close(np32(out), ref, REL_BF16, f"fp8 plain out {layout}")
+    rest = torch.cat([buf[:, :c0], buf[:, c0 + N:]], 1)
+    assert torch.isnan(rest.float()).all(), "a store landed outside the output view"
+
+
 def _experts_case(cfg, T=None, pairs_subset=None, fp8=False):
     moe = _moe()
     d = inputs(cfg, 0, T)
