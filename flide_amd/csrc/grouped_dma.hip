@@ -695,7 +695,7 @@ int launch_fp8_resident(GroupArgs& p, hipStream_t st) {
 //     and 3-7% (down) faster than 1 x 4 waves with 64-byte rows
 //  float8 (128-byte stage rows, one 128-wide MFMA step): bm 64 with BN = 128 and 2 stages (48 KB, three
 //     workgroups per CU); bm 128 in 8-wave workgroups: the plain (down) product 64 x 32 per wave, 2
-//     stages (375 -> 290 us at 4096 tokens; with K <= 768 grouped_fp8_resident replaces it, 190 us),
+//     stages (375 -> 290 us at 4096 tokens; with K <= 768 grouped_fp8_resident replaces it, 180 us),
 //     the gated (gate/up) product 64 x 64 per wave with BN = 256
 //     and 3 stages (144 KB; 5-10% faster than 2 x 2 waves of BN 128 at 4096-16384 tokens); bm 256:
 //     2 stages = 128 KB
