@@ -1,9 +1,8 @@
 // Sort and pad the (token, slot) pairs by expert: flide/kernels/moe.py:207-253 re-designed.
 //
-// The reference runs one program per expert, each scanning all n pairs (O(E n)). Here two launches do
-// O(n) work in total:
+// The reference runs one program per expert, each scanning all n pairs (O(E n)). Here the work is O(n):
+// up to ALIGN_FUSED_MAX pairs one launch of one workgroup (align_one, below); beyond that two launches:
 //   align_count  chunk c of ALIGN_CHUNK pairs -> an LDS histogram -> hist[c][E] in the workspace
-//                (skipped up to ALIGN_FUSED_MAX pairs: one align_place<true> then counts them itself)
 //   align_place  every chunk sums the histograms before it (and all of them, for the padded expert
 //                offsets), then places its pairs in pair order: each wave walks its quarter of the
 //                chunk 64 pairs at a time; lanes with the same expert find each other with log2(E+1)
@@ -37,7 +36,6 @@ __global__ __launch_bounds__(ALIGN_THREADS) void align_count(const int* __restri
   for (int e = threadIdx.x; e < E; e += ALIGN_THREADS) hist[(long long)blockIdx.x * E + e] = h[e];
 }
 
-template <bool FUSED>
 __global__ __launch_bounds__(ALIGN_THREADS) void align_place(const int* __restrict__ ids, int n, int E,
                                                              int bm, int nchunks,
                                                              const int* __restrict__ hist,
@@ -46,7 +44,134 @@ __global__ __launch_bounds__(ALIGN_THREADS) void align_place(const int* __restri
                                                              int* __restrict__ used,
                                                              int* __restrict__ counts) {
   __shared__ AlignShared<ALIGN_WAVES> S;
-  align_place_wg<FUSED, ALIGN_WAVES>(ids, n, E, bm, blockIdx.x, nchunks, hist, rows, blocks, used, counts, S);
+  align_place_wg<ALIGN_WAVES>(ids, n, E, bm, blockIdx.x, nchunks, hist, rows, blocks, used, counts, S);
+}
+
+// Up to ALIGN_FUSED_MAX pairs: one workgroup of 8 waves, one pass over the ids. Wave w owns the pairs
+// [w * wper, (w + 1) * wper), up to 8 per lane in 64-pair groups, held in registers from one load.
+//   1. each group's lanes with the same expert find each other with ballots; the lowest one adds the
+//      group's count to the wave's LDS counter for that expert, and every lane keeps its offset among
+//      the wave's pairs of that expert (counter before the group + rank in the group);
+//   2. one thread per expert: the total over waves, an exclusive scan of the padded totals (the
+//      segments' starts), the waves' bases inside the segment and the segment's blocks in an LDS
+//      block -> expert map;
+//   3. each pair's row is base + offset; the padding rows (the sentinel n) and the block map are written
+//      by all threads in strides, so no thread loops over an expert's padding alone.
+// 64 tokens x 8: 6.1 us for the two-pass form with 4 waves (ids loaded twice, an expert's padding
+// written by one thread).
+constexpr int ALIGN1_WAVES = 8;
+constexpr int ALIGN1_THREADS = ALIGN1_WAVES * 64;
+constexpr int ALIGN1_PER_LANE = ALIGN_FUSED_MAX / ALIGN1_THREADS;
+constexpr int ALIGN1_MAX_BLOCKS = ALIGN_FUSED_MAX + ALIGN_MAX_E;   // >= ceil((n + E (bm - 1)) / bm)
+
+__global__ __launch_bounds__(ALIGN1_THREADS) void align_one(const int* __restrict__ ids, int n, int E, int bm,
+                                                            int* __restrict__ rows, int* __restrict__ blocks,
+                                                            int* __restrict__ used, int* __restrict__ counts) {
+  __shared__ int wcnt[ALIGN1_WAVES][ALIGN_MAX_E];   // per wave: pairs per expert, then its base
+  __shared__ int start[ALIGN_MAX_E], cnt[ALIGN_MAX_E];
+  __shared__ int bexp[ALIGN1_MAX_BLOCKS];
+  __shared__ int scan_tmp[ALIGN1_WAVES];
+  __shared__ int s_used;
+  const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63;
+  const int wper = (n + ALIGN1_THREADS - 1) / ALIGN1_THREADS * 64;   // pairs per wave, whole groups
+  const int ng = wper / 64;                                          // groups per wave (<= 8)
+  const int wbase = wave * wper;
+
+  int e_g[ALIGN1_PER_LANE];
+#pragma unroll
+  for (int g = 0; g < ALIGN1_PER_LANE; ++g) {
+    if (g >= ng) break;
+    e_g[g] = ids[min(wbase + g * 64 + l, n - 1)];   // in bounds; a lane past n is dropped below
+  }
+  for (int w = 0; w < ALIGN1_WAVES; ++w)
+    for (int e = tid; e < E; e += ALIGN1_THREADS) wcnt[w][e] = 0;
+  __syncthreads();
+
+  int nbits = 1;
+  while ((1 << nbits) <= E) ++nbits;  // ids and the stand-in E fit in nbits
+  const unsigned long long lt = (l == 0) ? 0ull : (~0ull >> (64 - l));
+  int off_g[ALIGN1_PER_LANE];
+#pragma unroll
+  for (int g = 0; g < ALIGN1_PER_LANE; ++g) {
+    if (g >= ng) break;
+    int e = e_g[g];
+    if (wbase + g * 64 + l >= n || (unsigned)e >= (unsigned)E) e = E;
+    e_g[g] = e;
+    unsigned long long same = ~0ull;
+    for (int b = 0; b < nbits; ++b) {
+      const unsigned long long bal = __ballot((e >> b) & 1);
+      same &= ((e >> b) & 1) ? bal : ~bal;
+    }
+    off_g[g] = 0;
+    if (e < E) {
+      const int rank = __popcll(same & lt);
+      const int old = wcnt[wave][e];   // every lane reads before the group's lowest lane writes
+      off_g[g] = old + rank;
+      if (rank == 0) wcnt[wave][e] = old + __popcll(same);
+    }
+  }
+  __syncthreads();
+
+  // one thread per expert (E <= 1024 = 2 per thread): totals, padded exclusive scan, wave bases
+  const bool pow2 = (bm & (bm - 1)) == 0;
+  const int sh = 31 - __clz(bm);
+  auto pad = [&](int c) { return pow2 ? (c + bm - 1) & ~(bm - 1) : (c + bm - 1) / bm * bm; };
+  constexpr int PER = ALIGN_MAX_E / ALIGN1_THREADS;
+  int tot[PER], run = 0;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int e = tid * PER + j;
+    tot[j] = 0;
+    if (e < E)
+      for (int w = 0; w < ALIGN1_WAVES; ++w) tot[j] += wcnt[w][e];
+    run += pad(tot[j]);
+  }
+  int incl = run;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int v = __shfl_up(incl, o);
+    if (l >= o) incl += v;
+  }
+  if (l == 63) scan_tmp[wave] = incl;
+  __syncthreads();
+  int acc = incl - run;
+  for (int w = 0; w < wave; ++w) acc += scan_tmp[w];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int e = tid * PER + j;
+    if (e >= E) break;
+    const int s = acc, p = pad(tot[j]);
+    start[e] = s;
+    cnt[e] = tot[j];
+    int a = s;
+    for (int w = 0; w < ALIGN1_WAVES; ++w) {
+      const int v = wcnt[w][e];
+      wcnt[w][e] = a;
+      a += v;
+    }
+    for (int b = pow2 ? s >> sh : s / bm, b1 = pow2 ? (s + p) >> sh : (s + p) / bm; b < b1; ++b) bexp[b] = e;
+    if (counts) counts[e] = tot[j];
+    if (e == E - 1) {
+      used[0] = s + p;
+      s_used = s + p;
+    }
+    acc += p;
+  }
+  __syncthreads();
+
+#pragma unroll
+  for (int g = 0; g < ALIGN1_PER_LANE; ++g) {
+    if (g >= ng) break;
+    const int e = e_g[g];
+    if (e < E) rows[wcnt[wave][e] + off_g[g]] = wbase + g * 64 + l;
+  }
+  const int u = s_used;
+  for (int r = tid; r < u; r += ALIGN1_THREADS) {
+    const int e = bexp[pow2 ? r >> sh : r / bm];
+    if (r >= start[e] + cnt[e]) rows[r] = n;
+  }
+  const int nb = pow2 ? u >> sh : u / bm;
+  for (int b = tid; b < nb; b += ALIGN1_THREADS) blocks[b] = bexp[b];
 }
 
 }  // namespace
@@ -68,14 +193,13 @@ extern "C" int flide_moe_align(const int* ids, int n, int E, int bm, int* rows, 
   const int nchunks = align_chunks(n);
   int* hist = (int*)workspace;
   if (nchunks == 1) {   // one workgroup counts and places every pair
-    align_place<true><<<1, ALIGN_THREADS, 0, st>>>(ids, n, E, bm, 1, hist, rows, blocks, used, counts);
+    align_one<<<1, ALIGN1_THREADS, 0, st>>>(ids, n, E, bm, rows, blocks, used, counts);
     FLIDE_CHECK_LAUNCH();
     return FLIDE_MOE_OK;
   }
   align_count<<<nchunks, ALIGN_THREADS, 0, st>>>(ids, n, E, hist);
   FLIDE_CHECK_LAUNCH();
-  align_place<false><<<nchunks, ALIGN_THREADS, 0, st>>>(ids, n, E, bm, nchunks, hist, rows, blocks, used,
-                                                        counts);
+  align_place<<<nchunks, ALIGN_THREADS, 0, st>>>(ids, n, E, bm, nchunks, hist, rows, blocks, used, counts);
   FLIDE_CHECK_LAUNCH();
   return FLIDE_MOE_OK;
 }

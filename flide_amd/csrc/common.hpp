@@ -108,8 +108,10 @@ FLIDE_DEV float wave_sum(float v) {
 // order, so the combination is commutative). Lanes with nothing left carry value -inf and index
 // INT_MAX, so they never win over a real entry.
 FLIDE_DEV void wave_argmax(float& v, int& i) {
+  // `|` and `&`, not `||` and `&&`: the short-circuit forms compile to exec-mask branches, three per
+  // step, and a top-8 selection runs 48 steps in one dependent chain (route: 6.3 -> 3.5 us at 64 tokens)
   auto pick = [](float& v, int& i, float ov, int oi) {
-    const bool take = (ov > v) || (ov == v && oi < i);
+    const bool take = (ov > v) | ((ov == v) & (oi < i));
     v = take ? ov : v;
     i = take ? oi : i;
   };

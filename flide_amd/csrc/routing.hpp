@@ -1,6 +1,5 @@
 // Device pieces of routing: the per-token top-k selection (flide/kernels/moe.py:172-204, route.hip)
-// and the placement of pairs into per-expert segments (moe.py:207-253, align.hip), the latter written
-// for any number of waves per workgroup.
+// and the chunked placement of pairs into per-expert segments (moe.py:207-253, align.hip).
 #pragma once
 #include <limits.h>
 
@@ -24,11 +23,25 @@ template <int EPL> FLIDE_DEV void load_logits(const float* __restrict__ row, int
   for (int i = 0; i < EPL; ++i) v[i] = l + 64 * i < E ? row[l + 64 * i] : -INFINITY;
 }
 
-// The per-expert scale at experts l + 64 i (1 without a scale), loaded once per wave.
+// The per-expert scale at experts l + 64 i (1 without a scale), loaded once per wave. The raw bits of
+// every element are loaded before any is converted: a conversion inside the dtype branch puts a wait
+// for all of the wave's loads (the logits' too) between one element's load and the next.
 template <int EPL> FLIDE_DEV void load_scales(const void* scale, int dtype, int E, float (&sc)[EPL]) {
   const int l = lane_id();
+  uint32_t raw[EPL];
+  if (dtype == FLIDE_F32) {
 #pragma unroll
-  for (int i = 0; i < EPL; ++i) sc[i] = scale && l + 64 * i < E ? load_scalar(scale, dtype, l + 64 * i) : 1.f;
+    for (int i = 0; i < EPL; ++i)
+      raw[i] = scale && l + 64 * i < E ? ((const uint32_t*)scale)[l + 64 * i] : 0x3f800000u;
+  } else {
+    const uint32_t one = dtype == FLIDE_BF16 ? 0x3f80u : 0x3c00u;
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) raw[i] = scale && l + 64 * i < E ? ((const u16*)scale)[l + 64 * i] : one;
+  }
+#pragma unroll
+  for (int i = 0; i < EPL; ++i)
+    sc[i] = dtype == FLIDE_F32 ? __uint_as_float(raw[i])
+            : dtype == FLIDE_BF16 ? bf16_to_f32((u16)raw[i]) : f16_to_f32((u16)raw[i]);
 }
 
 // One token's routing by one wave from its logits v: the k largest of E in descending order, ties to
@@ -98,9 +111,8 @@ template <int NW> struct AlignShared {
   int scan_tmp[NW];
 };
 
-// Placement by one workgroup of NW waves (chunk c of the two-launch path, or every pair when FUSED).
-// `ids` may point to global memory or to LDS.
-template <bool FUSED, int NW>
+// Placement of chunk c of the two-launch path by one workgroup of NW waves.
+template <int NW>
 FLIDE_DEV void align_place_wg(const int* __restrict__ ids, int n, int E, int bm, int c, int nchunks,
                               const int* __restrict__ hist, int* __restrict__ rows,
                               int* __restrict__ blocks, int* __restrict__ used, int* __restrict__ counts,
@@ -114,38 +126,21 @@ FLIDE_DEV void align_place_wg(const int* __restrict__ ids, int n, int E, int bm,
   const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63;
 
   const int cbase = c * ALIGN_CHUNK;
-  // this wave's pairs: 1/NW of the chunk (FUSED: of all n pairs, in 64-pair steps), in pair order
-  const int wper = FUSED ? (n + ALIGN_WAVES * 64 - 1) / (ALIGN_WAVES * 64) * 64 : ALIGN_PER_WAVE;
+  // this wave's pairs: 1/NW of the chunk, in pair order
+  const int wper = ALIGN_PER_WAVE;
   const int wbase = cbase + wave * wper;
   const int wend = min(n, wbase + wper);
-  if constexpr (FUSED) {
-    // one chunk holds every pair: count them here (per wave, which the placement needs anyway)
-    for (int e = l; e < E; e += 64) wcur[wave][e] = 0;
-    __syncthreads();
-    for (int i = wbase + l; i < wend; i += 64) {
-      int e = ids[i];
-      if ((unsigned)e < (unsigned)E) atomicAdd(&wcur[wave][e], 1);
-    }
-    __syncthreads();
-    for (int e = tid; e < E; e += ALIGN_THREADS) {
-      int tot = 0;
-      for (int w = 0; w < ALIGN_WAVES; ++w) tot += wcur[w][e];
-      before[e] = 0;
-      cnt[e] = tot;
-    }
-  } else {
-    // per-expert totals and the share of earlier chunks
-    for (int e = tid; e < E; e += ALIGN_THREADS) {
-      int b = 0, tot = 0;
+  // per-expert totals and the share of earlier chunks
+  for (int e = tid; e < E; e += ALIGN_THREADS) {
+    int b = 0, tot = 0;
 #pragma unroll 8
-      for (int j = 0; j < nchunks; ++j) {
-        int v = hist[(long long)j * E + e];
-        if (j < c) b += v;
-        tot += v;
-      }
-      before[e] = b;
-      cnt[e] = tot;
+    for (int j = 0; j < nchunks; ++j) {
+      int v = hist[(long long)j * E + e];
+      if (j < c) b += v;
+      tot += v;
     }
+    before[e] = b;
+    cnt[e] = tot;
   }
   __syncthreads();
   // exclusive scan of the padded counts over experts: each thread owns a run of ceil(E / 256); a
@@ -176,15 +171,13 @@ FLIDE_DEV void align_place_wg(const int* __restrict__ ids, int n, int E, int bm,
   __syncthreads();
 
   // each wave's quarter of the chunk: its own histogram first, so waves place in pair order
-  if constexpr (!FUSED) {
-    for (int e = l; e < E; e += 64) wcur[wave][e] = 0;
-    __syncthreads();
-    for (int i = wbase + l; i < wend; i += 64) {
-      int e = ids[i];
-      if ((unsigned)e < (unsigned)E) atomicAdd(&wcur[wave][e], 1);
-    }
-    __syncthreads();
+  for (int e = l; e < E; e += 64) wcur[wave][e] = 0;
+  __syncthreads();
+  for (int i = wbase + l; i < wend; i += 64) {
+    int e = ids[i];
+    if ((unsigned)e < (unsigned)E) atomicAdd(&wcur[wave][e], 1);
   }
+  __syncthreads();
   // wcur[w][e] <- start[e] + before[e] + pairs of waves < w in this chunk
   for (int e = tid; e < E; e += ALIGN_THREADS) {
     int a = start[e] + before[e];

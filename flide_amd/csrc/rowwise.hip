@@ -131,6 +131,50 @@ struct SandwichArgs {
   long long sxo;
 };
 
+// Both sums of a token's two norms, from one pair of barriers; each sum is the one block_sum gives.
+FLIDE_DEV float2 block_sum2(float a, float b, float* red) {
+  a = wave_sum(a);
+  b = wave_sum(b);
+  const int wave = threadIdx.x >> 6, l = threadIdx.x & 63;
+  __syncthreads();
+  if (l == 0) {
+    red[wave] = a;
+    red[4 + wave] = b;
+  }
+  __syncthreads();
+  return make_float2(red[0] + red[1] + red[2] + red[3], red[4] + red[5] + red[6] + red[7]);
+}
+
+// The float32 sum of a token's y rows for one group of four columns, in slot order.
+template <typename YT> struct YGroup;
+template <> struct YGroup<float> {
+  typedef float raw __attribute__((ext_vector_type(4)));
+  // y is read exactly once: float32 rows with non-temporal loads, which keep them from evicting what the
+  // other wavefronts' rows still need (combine_norm at 8192 tokens: 153 -> 134 us, 6.2 TB/s)
+  static FLIDE_DEV raw load(const float* row, int c4) { return __builtin_nontemporal_load((const raw*)row + c4); }
+  static FLIDE_DEV float4 f32(raw r) { return make_float4(r[0], r[1], r[2], r[3]); }
+};
+template <> struct YGroup<u16> {
+  typedef uint32_t raw __attribute__((ext_vector_type(2)));
+  // 16-bit rows with plain loads: faster for them when y comes from HBM (4096 tokens, bf16 y: 53 -> 40 us;
+  // no difference right after the down product, whose y the next read finds in the last-level cache)
+  static FLIDE_DEV raw load(const u16* row, int c4) { return *((const raw*)row + c4); }
+  static FLIDE_DEV float4 f32(raw r) {
+    return make_float4(bf16_to_f32(r[0] & 0xffff), bf16_to_f32(r[0] >> 16), bf16_to_f32(r[1] & 0xffff),
+                       bf16_to_f32(r[1] >> 16));
+  }
+};
+
+FLIDE_DEV float4 bf16x4_f32(uint2 r) {
+  return make_float4(bf16_to_f32(r.x & 0xffff), bf16_to_f32(r.x >> 16), bf16_to_f32(r.y & 0xffff),
+                     bf16_to_f32(r.y >> 16));
+}
+
+// Every load of the token is issued before the first one is used: the k rows of y, dense, both norm
+// weights and, with SW, h and the two sandwich weights. The loads stay unconditional so that nothing
+// waits between them (a load under a per-lane or per-slot branch is followed by a wait for all loads in
+// flight: three round trips per token, 4.9 us at 64 tokens): a lane past the row's end loads the row's
+// last group and slots k .. KMAX - 1 load slot k - 1 again, and neither value is used.
 template <typename YT, int KMAX, bool SW = false>
 __global__ __launch_bounds__(RW_THREADS) void combine_norm_bf16_kernel(const YT* __restrict__ y,
                                                                        const u16* __restrict__ dense,
@@ -140,58 +184,58 @@ __global__ __launch_bounds__(RW_THREADS) void combine_norm_bf16_kernel(const YT*
                                                                        int H, int k, float eps,
                                                                        SandwichArgs sw = {}) {
   constexpr int V = 4;  // float4 groups per thread: H <= 256 * 4 * 4
-  __shared__ float red[4];
+  typedef YGroup<YT> G;
+  __shared__ float red[8];
   const long long t = blockIdx.x;
   const int nv = H / 4;
+  typename G::raw yr[V][KMAX];
+  uint2 draw[V], a1r[V], a2r[V], hr[V], wpr[V], wnr[V];
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    if (v * RW_THREADS >= nv) break;   // the same for every lane
+    const int c4 = min((int)threadIdx.x + v * RW_THREADS, nv - 1);
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j) yr[v][j] = G::load(y + (t * k + (j < k ? j : k - 1)) * (long long)H, c4);
+    draw[v] = ((const uint2*)(dense + t * sd))[c4];
+    a1r[v] = ((const uint2*)w1)[c4];
+    a2r[v] = ((const uint2*)w2)[c4];
+    if constexpr (SW) {
+      hr[v] = ((const uint2*)(sw.h + t * sw.sh))[c4];
+      wpr[v] = ((const uint2*)sw.wp)[c4];
+      if (sw.wn) wnr[v] = ((const uint2*)sw.wn)[c4];
+    }
+  }
+  float sc = 1.f;
+  if constexpr (SW) {
+    if (sw.scale) sc = load_any(sw.scale, sw.scale_dtype, 0);
+  }
   float4 acc[V], dv[V];
   float ss = 0.f, dd = 0.f;
 #pragma unroll
   for (int v = 0; v < V; ++v) {
-    const int c4 = threadIdx.x + v * RW_THREADS;
     acc[v] = make_float4(0.f, 0.f, 0.f, 0.f);
     dv[v] = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (c4 >= nv) continue;
-    const uint2 draw = ((const uint2*)(dense + t * sd))[c4];
-    dv[v] = make_float4(bf16_to_f32(draw.x & 0xffff), bf16_to_f32(draw.x >> 16), bf16_to_f32(draw.y & 0xffff),
-                        bf16_to_f32(draw.y >> 16));
-    float4 yv[KMAX];
-#pragma unroll
-    for (int j = 0; j < KMAX; ++j) {
-      if (j >= k) break;
-      const long long row = (t * k + j) * (long long)H;
-      // y is read exactly once: float32 rows with non-temporal loads, which keep them from evicting
-      // what the other wavefronts' rows still need (combine_norm at 8192 tokens: 153 -> 134 us,
-      // 6.2 TB/s); 16-bit rows (8 bytes per lane) with plain loads, faster for them when y comes
-      // from HBM (4096 tokens, bf16 y: 53 -> 40 us; no difference right after the down product,
-      // whose y the next read finds mostly in the last-level cache)
-      if constexpr (std::is_same<YT, float>::value) {
-        typedef float f32x4v __attribute__((ext_vector_type(4)));
-        const f32x4v t = __builtin_nontemporal_load((const f32x4v*)(y + row) + c4);
-        yv[j] = make_float4(t[0], t[1], t[2], t[3]);
-      } else {
-        typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
-        const u32x2v raw = *((const u32x2v*)(y + row) + c4);
-        yv[j] = make_float4(bf16_to_f32(raw[0] & 0xffff), bf16_to_f32(raw[0] >> 16), bf16_to_f32(raw[1] & 0xffff),
-                            bf16_to_f32(raw[1] >> 16));
-      }
-    }
+    if (v * RW_THREADS >= nv) break;
+    if ((int)threadIdx.x + v * RW_THREADS >= nv) continue;
+    dv[v] = bf16x4_f32(draw[v]);
 #pragma unroll
     for (int j = 0; j < KMAX; ++j) {   // slot order
       if (j >= k) break;
-      acc[v].x += yv[j].x; acc[v].y += yv[j].y; acc[v].z += yv[j].z; acc[v].w += yv[j].w;
+      const float4 yv = G::f32(yr[v][j]);
+      acc[v].x += yv.x; acc[v].y += yv.y; acc[v].z += yv.z; acc[v].w += yv.w;
     }
     ss += acc[v].x * acc[v].x + acc[v].y * acc[v].y + acc[v].z * acc[v].z + acc[v].w * acc[v].w;
     dd += dv[v].x * dv[v].x + dv[v].y * dv[v].y + dv[v].z * dv[v].z + dv[v].w * dv[v].w;
   }
-  const float sum_ss = block_sum(ss, red);
-  const float sum_dd = block_sum(dd, red);
-  const float inv_b = rsqrtf(sum_ss / H + eps);
-  const float inv_a = rsqrtf(sum_dd / H + eps);
+  const float2 sums = block_sum2(ss, dd, red);
+  const float inv_b = rsqrtf(sums.x / H + eps);
+  const float inv_a = rsqrtf(sums.y / H + eps);
 #pragma unroll
   for (int v = 0; v < V; ++v) {
+    if (v * RW_THREADS >= nv) break;
     const int c4 = threadIdx.x + v * RW_THREADS;
     if (c4 >= nv) continue;
-    const uint2 a1 = ((const uint2*)w1)[c4], a2 = ((const uint2*)w2)[c4];
+    const uint2 a1 = a1r[v], a2 = a2r[v];
     const float o0 = dv[v].x * inv_a * bf16_to_f32(a1.x & 0xffff) + acc[v].x * inv_b * bf16_to_f32(a2.x & 0xffff);
     const float o1 = dv[v].y * inv_a * bf16_to_f32(a1.x >> 16) + acc[v].y * inv_b * bf16_to_f32(a2.x >> 16);
     const float o2 = dv[v].z * inv_a * bf16_to_f32(a1.y & 0xffff) + acc[v].z * inv_b * bf16_to_f32(a2.y & 0xffff);
@@ -200,8 +244,7 @@ __global__ __launch_bounds__(RW_THREADS) void combine_norm_bf16_kernel(const YT*
     o.x = (uint32_t)f32_to_bf16(o0) | ((uint32_t)f32_to_bf16(o1) << 16);
     o.y = (uint32_t)f32_to_bf16(o2) | ((uint32_t)f32_to_bf16(o3) << 16);
     if constexpr (SW) {
-      dv[v] = make_float4(bf16_to_f32(o.x & 0xffff), bf16_to_f32(o.x >> 16), bf16_to_f32(o.y & 0xffff),
-                          bf16_to_f32(o.y >> 16));   // d, rounded as the reference stores it
+      dv[v] = bf16x4_f32(o);   // d, rounded as the reference stores it
     } else {
       ((uint2*)(out + t * so))[c4] = o;
     }
@@ -210,20 +253,19 @@ __global__ __launch_bounds__(RW_THREADS) void combine_norm_bf16_kernel(const YT*
     float d2 = 0.f;
 #pragma unroll
     for (int v = 0; v < V; ++v) {
-      const int c4 = threadIdx.x + v * RW_THREADS;
-      if (c4 >= nv) continue;
+      if (v * RW_THREADS >= nv) break;
+      if ((int)threadIdx.x + v * RW_THREADS >= nv) continue;
       d2 += dv[v].x * dv[v].x + dv[v].y * dv[v].y + dv[v].z * dv[v].z + dv[v].w * dv[v].w;
     }
     const float inv_d = rsqrtf(block_sum(d2, red) / H + eps);
-    const float sc = sw.scale ? load_any(sw.scale, sw.scale_dtype, 0) : 1.f;
     float h2 = 0.f;
 #pragma unroll
     for (int v = 0; v < V; ++v) {
+      if (v * RW_THREADS >= nv) break;
       const int c4 = threadIdx.x + v * RW_THREADS;
       if (c4 >= nv) continue;
-      const uint2 hr = ((const uint2*)(sw.h + t * sw.sh))[c4], wr = ((const uint2*)sw.wp)[c4];
       const float dq[4] = {dv[v].x, dv[v].y, dv[v].z, dv[v].w};
-      const uint32_t hu[2] = {hr.x, hr.y}, wu[2] = {wr.x, wr.y};
+      const uint32_t hu[2] = {hr[v].x, hr[v].y}, wu[2] = {wpr[v].x, wpr[v].y};
       float hb[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -244,9 +286,10 @@ __global__ __launch_bounds__(RW_THREADS) void combine_norm_bf16_kernel(const YT*
       const float inv_h = rsqrtf(block_sum(h2, red) / H + eps);
 #pragma unroll
       for (int v = 0; v < V; ++v) {
+        if (v * RW_THREADS >= nv) break;
         const int c4 = threadIdx.x + v * RW_THREADS;
         if (c4 >= nv) continue;
-        const uint2 wr = ((const uint2*)sw.wn)[c4];
+        const uint2 wr = wnr[v];
         uint2 o;
         o.x = (uint32_t)f32_to_bf16(dv[v].x * inv_h * bf16_to_f32(wr.x & 0xffff)) |
               ((uint32_t)f32_to_bf16(dv[v].y * inv_h * bf16_to_f32(wr.x >> 16)) << 16);
@@ -256,6 +299,17 @@ __global__ __launch_bounds__(RW_THREADS) void combine_norm_bf16_kernel(const YT*
       }
     }
   }
+}
+
+// KMAX: the loads a lane issues per group of columns (k rounded up to 2, 4 or 8)
+template <typename YT, bool SW>
+void launch_combine_norm_vec(const YT* y, const u16* dense, long long sd, const u16* w1, const u16* w2, u16* out,
+                             long long so, int T, int H, int k, float eps, SandwichArgs sw, hipStream_t st) {
+#define CN(KM) combine_norm_bf16_kernel<YT, KM, SW><<<T, RW_THREADS, 0, st>>>(y, dense, sd, w1, w2, out, so, H, k, eps, sw)
+  if (k <= 2) CN(2);
+  else if (k <= 4) CN(4);
+  else CN(8);
+#undef CN
 }
 
 // combine (Qwen), vectorised for y float32 or bf16 with bf16 shared and out, H % 4 == 0, H <= 4096 and
@@ -487,16 +541,14 @@ extern "C" int flide_moe_combine_norm(const void* y, int y_dtype, const void* de
   const bool vec = out_dtype == FLIDE_BF16 && w_dtype == FLIDE_BF16 && H <= 4 * 4 * RW_THREADS && k <= 8 &&
                    sd % 4 == 0 && so % 4 == 0 && !(((uintptr_t)dense | (uintptr_t)out | (uintptr_t)w1 | (uintptr_t)w2) & 7);
   if (vec && y_dtype == FLIDE_F32) {
-    combine_norm_bf16_kernel<float, 8><<<T, RW_THREADS, 0, st>>>((const float*)y, (const u16*)dense, sd,
-                                                                 (const u16*)w1, (const u16*)w2, (u16*)out, so,
-                                                                 H, k, eps);
+    launch_combine_norm_vec<float, false>((const float*)y, (const u16*)dense, sd, (const u16*)w1, (const u16*)w2,
+                                          (u16*)out, so, T, H, k, eps, {}, st);
     FLIDE_CHECK_LAUNCH();
     return FLIDE_MOE_OK;
   }
   if (vec && y_dtype == FLIDE_BF16) {
-    combine_norm_bf16_kernel<u16, 8><<<T, RW_THREADS, 0, st>>>((const u16*)y, (const u16*)dense, sd,
-                                                               (const u16*)w1, (const u16*)w2, (u16*)out, so,
-                                                               H, k, eps);
+    launch_combine_norm_vec<u16, false>((const u16*)y, (const u16*)dense, sd, (const u16*)w1, (const u16*)w2,
+                                        (u16*)out, so, T, H, k, eps, {}, st);
     FLIDE_CHECK_LAUNCH();
     return FLIDE_MOE_OK;
   }
@@ -671,11 +723,11 @@ extern "C" int flide_moe_combine_norm_sandwich(const void* y, int y_dtype, const
                         (u16*)h_out, sho, (u16*)x_out, sxo};
   hipStream_t st = (hipStream_t)stream;
   if (y_dtype == FLIDE_F32)
-    combine_norm_bf16_kernel<float, 8, true><<<T, RW_THREADS, 0, st>>>(
-        (const float*)y, (const u16*)dense, sd, (const u16*)w1, (const u16*)w2, nullptr, 0, H, k, eps, sw);
+    launch_combine_norm_vec<float, true>((const float*)y, (const u16*)dense, sd, (const u16*)w1, (const u16*)w2,
+                                         nullptr, 0, T, H, k, eps, sw, st);
   else
-    combine_norm_bf16_kernel<u16, 8, true><<<T, RW_THREADS, 0, st>>>(
-        (const u16*)y, (const u16*)dense, sd, (const u16*)w1, (const u16*)w2, nullptr, 0, H, k, eps, sw);
+    launch_combine_norm_vec<u16, true>((const u16*)y, (const u16*)dense, sd, (const u16*)w1, (const u16*)w2,
+                                       nullptr, 0, T, H, k, eps, sw, st);
   FLIDE_CHECK_LAUNCH();
   return FLIDE_MOE_OK;
 }

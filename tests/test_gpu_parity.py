@@ -86,7 +86,8 @@ def _check_align(ids_np, E, bm):
 
 
 @pytest.mark.parametrize("T,E,k,bm", [(64, 128, 8, 16), (256, 16, 2, 64), (5000, 128, 8, 128), (3, 7, 2, 1),
-                                      (1000, 1000, 4, 32), (2048, 128, 8, 128)])
+                                      (1000, 1000, 4, 32), (2048, 128, 8, 128), (512, 128, 8, 48),
+                                      (700, 60, 3, 24), (1, 128, 8, 128), (513, 128, 8, 32)])
 def test_align_random(T, E, k, bm):
     print(f"align T={T} E={E} k={k} bm={bm}", flush=True)
     rng = np.random.default_rng(T + E)
@@ -384,17 +385,20 @@ def test_experts_cfg3_fp8_decode_tile():
 # --------------------------------------------------------------------------------------------------
 # combine, quantize, router, norms
 # --------------------------------------------------------------------------------------------------
-def test_combine_norm():
-    print("combine_norm", flush=True)
+@pytest.mark.parametrize("T,H,k,ydt", [(37, 2816, 8, torch.float32), (29, 1024, 2, torch.float32),
+                                       (19, 2048 + 64, 3, torch.bfloat16), (11, 4096, 5, torch.float32),
+                                       (7, 1000, 1, torch.bfloat16), (5, 2816, 4, torch.bfloat16)])
+def test_combine_norm(T, H, k, ydt):
+    """The vector kernel at every per-lane load count (k up to 2, 4 and 8), ragged H, f32 and bf16 y."""
+    print(f"combine_norm T={T} H={H} k={k} y {ydt}", flush=True)
     moe = _moe()
     g = torch.Generator().manual_seed(11)
-    T, H, k = 37, 2816, 8
-    y = torch.randn(T * k, H, generator=g)
+    y = torch.randn(T * k, H, generator=g).to(ydt)
     dense = torch.randn(T, H, generator=g).to(torch.bfloat16)
     w1 = (torch.rand(H, generator=g) + 0.5).to(torch.bfloat16)
     w2 = (torch.rand(H, generator=g) + 0.5).to(torch.bfloat16)
     out = moe.combine_norm(y.to(DEV), dense.to(DEV), w1.to(DEV), w2.to(DEV), k, 1e-6)
-    ref = orc.combine_norm(y.numpy(), np32(dense), np32(w1), np32(w2), k, 1e-6)
+    ref = orc.combine_norm(np32(y), np32(dense), np32(w1), np32(w2), k, 1e-6)
     assert_close(np32(out), ref, 1e-2, "combine_norm")
     # one bf16 rounding: at most 1 ulp from the float64 reference
     np.testing.assert_allclose(np32(out), ref, rtol=2 ** -7, atol=1e-6)
