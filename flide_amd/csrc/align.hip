@@ -7,8 +7,8 @@
 //                offsets), then places its pairs in pair order: each wave walks its quarter of the
 //                chunk 64 pairs at a time; lanes with the same expert find each other with log2(E+1)
 //                ballots, rank themselves by lane order and bump the wave's LDS counter once.
-//                Chunk 0's workgroup also writes the padding sentinels, the block -> expert map,
-//                `used` and the counts.
+//                Chunk c also writes, for experts e = c, c + nchunks, ..., the padding sentinels,
+//                the block -> expert map and the counts (and `used` with the last expert).
 // The result is the reference's layout exactly: per expert its pairs in ascending pair order, then the
 // sentinel n up to a multiple of bm.
 #include "routing.hpp"
@@ -43,8 +43,126 @@ __global__ __launch_bounds__(ALIGN_THREADS) void align_place(const int* __restri
                                                              int* __restrict__ blocks,
                                                              int* __restrict__ used,
                                                              int* __restrict__ counts) {
-  __shared__ AlignShared<ALIGN_WAVES> S;
-  align_place_wg<ALIGN_WAVES>(ids, n, E, bm, blockIdx.x, nchunks, hist, rows, blocks, used, counts, S);
+  constexpr int PL = ALIGN_PER_WAVE / 64;   // pairs per lane
+  __shared__ int start[ALIGN_MAX_E];    // padded start of each expert's segment
+  __shared__ int before[ALIGN_MAX_E];   // this expert's pairs in earlier chunks
+  __shared__ int cnt[ALIGN_MAX_E];      // total pairs per expert
+  __shared__ int wcnt[ALIGN_WAVES][ALIGN_MAX_E];   // per wave: its pairs per expert, then its base
+  __shared__ int scan_tmp[ALIGN_WAVES];
+  const int c = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, l = tid & 63;
+  // the wave's pairs [wbase, wbase + 256), 4 per lane in 64-pair groups, loaded once and held in registers
+  const int wbase = c * ALIGN_CHUNK + wave * ALIGN_PER_WAVE;
+  int e_g[PL];
+#pragma unroll
+  for (int g = 0; g < PL; ++g) e_g[g] = ids[min(wbase + g * 64 + l, n - 1)];   // in bounds; past n dropped below
+  // per-expert totals and the share of earlier chunks: the whole histogram matrix [nchunks][E], read by
+  // every thread in a strided share with 16 loads in flight (issued with the ids), added into LDS
+  const int total = nchunks * E;
+  int hv[16];
+#pragma unroll
+  for (int u = 0; u < 16; ++u) {
+    const int i = tid + u * ALIGN_THREADS;
+    hv[u] = i < total ? hist[i] : 0;
+  }
+  for (int e = tid; e < E; e += ALIGN_THREADS) {
+    before[e] = 0;
+    cnt[e] = 0;
+#pragma unroll
+    for (int w = 0; w < ALIGN_WAVES; ++w) wcnt[w][e] = 0;
+  }
+  __syncthreads();
+  for (int i0 = tid;; ) {
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      if (hv[u] == 0) continue;
+      const int i = i0 + u * ALIGN_THREADS, j = i / E, e = i - j * E;
+      atomicAdd(&cnt[e], hv[u]);
+      if (j < c) atomicAdd(&before[e], hv[u]);
+    }
+    i0 += ALIGN_THREADS * 16;
+    if (i0 >= total) break;
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int i = i0 + u * ALIGN_THREADS;
+      hv[u] = i < total ? hist[i] : 0;
+    }
+  }
+  // the wave's own pairs per expert, and each lane's offset among the wave's pairs of its expert: lanes
+  // of a 64-pair group with the same expert find each other with log2(E+1) ballots; the lowest adds the
+  // group's count (every lane reads the counter before the lowest one writes it)
+  int nbits = 1;
+  while ((1 << nbits) <= E) ++nbits;  // ids and the stand-in E fit in nbits
+  const unsigned long long lt = (l == 0) ? 0ull : (~0ull >> (64 - l));
+  int off_g[PL];
+#pragma unroll
+  for (int g = 0; g < PL; ++g) {
+    int e = e_g[g];
+    if (wbase + g * 64 + l >= n || (unsigned)e >= (unsigned)E) e = E;
+    e_g[g] = e;
+    unsigned long long same = ~0ull;
+    for (int b = 0; b < nbits; ++b) {
+      const unsigned long long bal = __ballot((e >> b) & 1);
+      same &= ((e >> b) & 1) ? bal : ~bal;
+    }
+    off_g[g] = 0;
+    if (e < E) {
+      const int rank = __popcll(same & lt);
+      const int old = wcnt[wave][e];
+      off_g[g] = old + rank;
+      if (rank == 0) wcnt[wave][e] = old + __popcll(same);
+    }
+  }
+  __syncthreads();
+  // exclusive scan of the padded counts over experts: each thread owns a run of ceil(E / 256); a
+  // shuffle scan inside each wave, then the waves' totals
+  const int per = (E + ALIGN_THREADS - 1) / ALIGN_THREADS;
+  int run = 0;
+  for (int j = 0; j < per; ++j) {
+    const int e = tid * per + j;
+    if (e < E) run += (cnt[e] + bm - 1) / bm * bm;
+  }
+  int incl = run;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int v = __shfl_up(incl, o);
+    if (l >= o) incl += v;
+  }
+  if (l == 63) scan_tmp[wave] = incl;
+  __syncthreads();
+  int acc = incl - run;
+  for (int w = 0; w < wave; ++w) acc += scan_tmp[w];
+  for (int j = 0; j < per; ++j) {
+    const int e = tid * per + j;
+    if (e < E) {
+      start[e] = acc;
+      // wcnt[w][e] <- start[e] + before[e] + pairs of waves < w in this chunk
+      int a = acc + before[e];
+#pragma unroll
+      for (int w = 0; w < ALIGN_WAVES; ++w) {
+        const int v = wcnt[w][e];
+        wcnt[w][e] = a;
+        a += v;
+      }
+      acc += (cnt[e] + bm - 1) / bm * bm;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int g = 0; g < PL; ++g)
+    if (e_g[g] < E) rows[wcnt[wave][e_g[g]] + off_g[g]] = wbase + g * 64 + l;
+
+  // experts c, c + nchunks, ...: sentinels after the pairs, the block -> expert map, the counts; every
+  // thread of the workgroup takes a stride of each expert's rows and blocks
+  for (int e = c; e < E; e += nchunks) {
+    const int s = start[e], ce = cnt[e];
+    const int p = (ce + bm - 1) / bm * bm;
+    for (int r = s + ce + tid; r < s + p; r += ALIGN_THREADS) rows[r] = n;
+    for (int b = s / bm + tid; b < (s + p) / bm; b += ALIGN_THREADS) blocks[b] = e;
+    if (tid == 0) {
+      if (counts) counts[e] = ce;
+      if (e == E - 1) used[0] = s + p;
+    }
+  }
 }
 
 // Up to ALIGN_FUSED_MAX pairs: one workgroup of 8 waves, one pass over the ids. Wave w owns the pairs

@@ -135,6 +135,34 @@ FLIDE_DEV void wave_argmax(float& v, int& i) {
   }
 }
 
+// The same reductions inside each row of 16 lanes (the four DPP steps above): every lane ends with its
+// row's result, so a wave can carry four independent 16-lane groups.
+FLIDE_DEV float row16_max(float v) {
+  v = fmaxf(v, __int_as_float(dpp_xor1(__float_as_int(v))));
+  v = fmaxf(v, __int_as_float(dpp_xor2(__float_as_int(v))));
+  v = fmaxf(v, __int_as_float(dpp_half_mirror(__float_as_int(v))));
+  return fmaxf(v, __int_as_float(dpp_mirror(__float_as_int(v))));
+}
+
+FLIDE_DEV float row16_sum(float v) {
+  v += __int_as_float(dpp_xor1(__float_as_int(v)));
+  v += __int_as_float(dpp_xor2(__float_as_int(v)));
+  v += __int_as_float(dpp_half_mirror(__float_as_int(v)));
+  return v + __int_as_float(dpp_mirror(__float_as_int(v)));
+}
+
+FLIDE_DEV void row16_argmax(float& v, int& i) {
+  auto pick = [](float& v, int& i, float ov, int oi) {
+    const bool take = (ov > v) | ((ov == v) & (oi < i));
+    v = take ? ov : v;
+    i = take ? oi : i;
+  };
+  pick(v, i, __int_as_float(dpp_xor1(__float_as_int(v))), dpp_xor1(i));
+  pick(v, i, __int_as_float(dpp_xor2(__float_as_int(v))), dpp_xor2(i));
+  pick(v, i, __int_as_float(dpp_half_mirror(__float_as_int(v))), dpp_half_mirror(i));
+  pick(v, i, __int_as_float(dpp_mirror(__float_as_int(v))), dpp_mirror(i));
+}
+
 FLIDE_DEV int lane_id() { return (int)__lane_id(); }
 
 // ---------------------------------------------------------------------------------------------------

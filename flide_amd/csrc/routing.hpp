@@ -1,5 +1,5 @@
 // Device pieces of routing: the per-token top-k selection (flide/kernels/moe.py:172-204, route.hip)
-// and the chunked placement of pairs into per-expert segments (moe.py:207-253, align.hip).
+// and the constants of the placement of pairs into per-expert segments (moe.py:207-253, align.hip).
 #pragma once
 #include <limits.h>
 
@@ -102,125 +102,5 @@ FLIDE_DEV void route_select(const float (&v)[EPL], const float (&sc)[EPL], int E
     if (idlds) idlds[l] = my_id;
   }
 }
-
-template <int NW> struct AlignShared {
-  int start[ALIGN_MAX_E];    // padded start of each expert's segment
-  int before[ALIGN_MAX_E];   // this expert's pairs in earlier chunks
-  int cnt[ALIGN_MAX_E];      // total pairs per expert
-  int wcur[NW][ALIGN_MAX_E];
-  int scan_tmp[NW];
-};
-
-// Placement of chunk c of the two-launch path by one workgroup of NW waves.
-template <int NW>
-FLIDE_DEV void align_place_wg(const int* __restrict__ ids, int n, int E, int bm, int c, int nchunks,
-                              const int* __restrict__ hist, int* __restrict__ rows,
-                              int* __restrict__ blocks, int* __restrict__ used, int* __restrict__ counts,
-                              AlignShared<NW>& S) {
-  constexpr int ALIGN_THREADS = NW * 64, ALIGN_WAVES = NW, ALIGN_CHUNK = NW * ALIGN_PER_WAVE;
-  int* const start = S.start;
-  int* const before = S.before;
-  int* const cnt = S.cnt;
-  int (*const wcur)[ALIGN_MAX_E] = S.wcur;
-  int* const scan_tmp = S.scan_tmp;
-  const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63;
-
-  const int cbase = c * ALIGN_CHUNK;
-  // this wave's pairs: 1/NW of the chunk, in pair order
-  const int wper = ALIGN_PER_WAVE;
-  const int wbase = cbase + wave * wper;
-  const int wend = min(n, wbase + wper);
-  // per-expert totals and the share of earlier chunks
-  for (int e = tid; e < E; e += ALIGN_THREADS) {
-    int b = 0, tot = 0;
-#pragma unroll 8
-    for (int j = 0; j < nchunks; ++j) {
-      int v = hist[(long long)j * E + e];
-      if (j < c) b += v;
-      tot += v;
-    }
-    before[e] = b;
-    cnt[e] = tot;
-  }
-  __syncthreads();
-  // exclusive scan of the padded counts over experts: each thread owns a run of ceil(E / 256); a
-  // shuffle scan inside each wave, then the waves' totals
-  const int per = (E + ALIGN_THREADS - 1) / ALIGN_THREADS;
-  int run = 0;
-  for (int j = 0; j < per; ++j) {
-    int e = tid * per + j;
-    if (e < E) run += (cnt[e] + bm - 1) / bm * bm;
-  }
-  int incl = run;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int v = __shfl_up(incl, o);
-    if (l >= o) incl += v;
-  }
-  if (l == 63) scan_tmp[wave] = incl;
-  __syncthreads();
-  int acc = incl - run;
-  for (int w = 0; w < wave; ++w) acc += scan_tmp[w];
-  for (int j = 0; j < per; ++j) {
-    int e = tid * per + j;
-    if (e < E) {
-      start[e] = acc;
-      acc += (cnt[e] + bm - 1) / bm * bm;
-    }
-  }
-  __syncthreads();
-
-  // each wave's quarter of the chunk: its own histogram first, so waves place in pair order
-  for (int e = l; e < E; e += 64) wcur[wave][e] = 0;
-  __syncthreads();
-  for (int i = wbase + l; i < wend; i += 64) {
-    int e = ids[i];
-    if ((unsigned)e < (unsigned)E) atomicAdd(&wcur[wave][e], 1);
-  }
-  __syncthreads();
-  // wcur[w][e] <- start[e] + before[e] + pairs of waves < w in this chunk
-  for (int e = tid; e < E; e += ALIGN_THREADS) {
-    int a = start[e] + before[e];
-    for (int w = 0; w < ALIGN_WAVES; ++w) {
-      int v = wcur[w][e];
-      wcur[w][e] = a;
-      a += v;
-    }
-  }
-  __syncthreads();
-
-  int nbits = 1;
-  while ((1 << nbits) <= E) ++nbits;  // ids and the sentinel E fit in nbits
-  const unsigned long long lt = (l == 0) ? 0ull : (~0ull >> (64 - l));
-  for (int i0 = wbase; i0 < wend; i0 += 64) {
-    const int i = i0 + l;
-    int e = i < wend ? ids[i] : E;
-    if ((unsigned)e >= (unsigned)E) e = E;
-    unsigned long long same = ~0ull;
-    for (int b = 0; b < nbits; ++b) {
-      unsigned long long bal = __ballot((e >> b) & 1);
-      same &= ((e >> b) & 1) ? bal : ~bal;
-    }
-    if (e < E) {
-      const int rank = __popcll(same & lt);
-      const int old = wcur[wave][e];
-      rows[old + rank] = i;
-      if (rank == 0) wcur[wave][e] = old + __popcll(same);
-    }
-  }
-
-  // chunk 0: sentinels, block map, counts, used
-  if (c == 0) {
-    for (int e = tid; e < E; e += ALIGN_THREADS) {
-      const int s = start[e], ce = cnt[e];
-      const int p = (ce + bm - 1) / bm * bm;
-      for (int r = s + ce; r < s + p; ++r) rows[r] = n;
-      for (int b = s / bm; b < (s + p) / bm; ++b) blocks[b] = e;
-      if (counts) counts[e] = ce;
-      if (e == E - 1) used[0] = s + p;
-    }
-  }
-}
-
 
 }  // namespace routing

@@ -32,7 +32,8 @@ def _gelu_act(gu, n):
 # --------------------------------------------------------------------------------------------------
 # routing
 # --------------------------------------------------------------------------------------------------
-@pytest.mark.parametrize("T,E,k", [(1, 16, 2), (64, 128, 8), (300, 96, 6), (257, 1000, 4), (8, 8, 8), (33, 5, 1)])
+@pytest.mark.parametrize("T,E,k", [(1, 16, 2), (64, 128, 8), (300, 96, 6), (257, 1000, 4), (8, 8, 8), (33, 5, 1),
+                                   (2048, 16, 2), (2500, 96, 6), (2049, 128, 16), (3001, 5, 1), (4096, 33, 3)])
 def test_route_matches_oracle(T, E, k):
     print(f"route T={T} E={E} k={k}", flush=True)
     g = torch.Generator().manual_seed(T * 7 + E)
@@ -44,10 +45,12 @@ def test_route_matches_oracle(T, E, k):
     np.testing.assert_allclose(w.cpu().numpy(), rw, rtol=1e-5, atol=1e-7)
 
 
-def test_route_ties_go_to_lower_id():
-    print("route ties", flush=True)
+@pytest.mark.parametrize("T", [512, 4096])
+def test_route_ties_go_to_lower_id(T):
+    """Both route kernels (one token per wave below 2048 tokens, four per wave from there)."""
+    print(f"route ties T={T}", flush=True)
     g = torch.Generator().manual_seed(5)
-    logits = torch.randint(-3, 3, (512, 128), generator=g).float()   # heavy exact ties
+    logits = torch.randint(-3, 3, (T, 128), generator=g).float()   # heavy exact ties
     logits[0] = 0.0                                                   # all equal: ids 0..k-1, weights 1/k
     w, ids = _moe().route(logits.to(DEV), 8)
     rw, rids = orc.route(logits.numpy(), 8)
