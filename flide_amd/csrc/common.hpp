@@ -71,6 +71,53 @@ FLIDE_DEV float e4m3fn_to_f32(u8 c) {
   return __uint_as_float(s | ((e + 120u) << 23) | (m << 20));
 }
 
+// x / sc with the bits of the correctly rounded float32 division, in three operations instead of the
+// division's ten: q0 = x * (1/sc) is within about an ulp of the quotient, and one correction from the
+// exact residual x - q0*sc (an fma) rounds to the correctly rounded quotient (Markstein's theorem for a
+// correctly rounded reciprocal and a faithful first quotient). The residual is x - q0*sc negated so that
+// x = -0 keeps its sign (nrinv = -1/sc). For 16-bit x and the scales the quantiser makes (sc from a
+// 16-bit amax) the result was compared with the division on every (x, amax) pair of bfloat16 and of
+// float16: identical wherever |x / sc| > 2^-11, and elsewhere the same sign (both encode to +-0 in
+// e4m3). sc must be finite: an inf in the row makes sc inf and the residual NaN, which the caller handles
+// with the division.
+FLIDE_DEV float div_markstein(float x, float sc, float rinv, float nrinv) {
+  const float q0 = x * rinv;
+  return __builtin_fmaf(__builtin_fmaf(q0, sc, -x), nrinv, q0);
+}
+
+// One 16-byte piece of a 16-bit row (8 values, bf16 or f16) quantized by the row's scale sc: x / sc
+// (div_markstein when sc is finite, else the division), clamped to +-448, rounded to e4m3fn bytes by
+// gfx950's packed conversion (round to nearest even; on clamped inputs it gives f32_to_e4m3fn's bytes,
+// checked on every code, every tie and its neighbours). rinv = 1 / sc, nrinv = -rinv.
+template <bool BF16, bool FINITE>
+FLIDE_DEV uint2 quantize_piece8(const uint4& raw, float sc, float rinv, float nrinv) {
+  const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+  float t[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const u16 h = (i & 1) ? (u16)(w[i >> 1] >> 16) : (u16)(w[i >> 1] & 0xffff);
+    const float xv = BF16 ? bf16_to_f32(h) : f16_to_f32(h);
+    t[i] = FINITE ? div_markstein(xv, sc, rinv, nrinv) : xv / sc;
+    t[i] = fminf(fmaxf(t[i], -448.0f), 448.0f);
+  }
+  uint32_t lo = __builtin_amdgcn_cvt_pk_fp8_f32(t[0], t[1], 0u, false);
+  lo = __builtin_amdgcn_cvt_pk_fp8_f32(t[2], t[3], lo, true);
+  uint32_t hi = __builtin_amdgcn_cvt_pk_fp8_f32(t[4], t[5], 0u, false);
+  hi = __builtin_amdgcn_cvt_pk_fp8_f32(t[6], t[7], hi, true);
+  return make_uint2(lo, hi);
+}
+
+// The largest |value| of a 16-byte piece of 16-bit values.
+template <bool BF16> FLIDE_DEV float piece8_amax(const uint4& raw, float amax) {
+  const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const u16 h = (i & 1) ? (u16)(w[i >> 1] >> 16) : (u16)(w[i >> 1] & 0xffff);
+    amax = fmaxf(amax, fabsf(BF16 ? bf16_to_f32(h) : f16_to_f32(h)));
+  }
+  return amax;
+}
+
 // ---------------------------------------------------------------------------------------------------
 // wave64 reductions
 // ---------------------------------------------------------------------------------------------------

@@ -401,47 +401,15 @@ __global__ __launch_bounds__(RW_THREADS) void quantize_rows_kernel(const void* _
   }
 }
 
-// x / sc with the bits of the correctly rounded float32 division, in three operations instead of the
-// division's ten: q0 = x * (1/sc) is within about an ulp of the quotient, and one correction from the
-// exact residual x - q0*sc (an fma) rounds to the correctly rounded quotient (Markstein's theorem for a
-// correctly rounded reciprocal and a faithful first quotient). The residual is x - q0*sc negated so that
-// x = -0 keeps its sign (nrinv = -1/sc). For 16-bit x and the scales the quantiser makes (sc from a
-// 16-bit amax) the result was compared with the division on every (x, amax) pair of bfloat16 and of
-// float16: identical wherever |x / sc| > 2^-11, and elsewhere the same sign (both encode to +-0 in
-// e4m3). sc must be finite: an inf in the row makes sc inf and the residual NaN, which the caller handles
-// with the division.
-FLIDE_DEV float div_markstein(float x, float sc, float rinv, float nrinv) {
-  const float q0 = x * rinv;
-  return __builtin_fmaf(__builtin_fmaf(q0, sc, -x), nrinv, q0);
-}
-
 // quantize_rows_vec_kernel's second pass: the row's pieces (already in registers) to e4m3 bytes.
 template <int NV, bool BF16, bool FINITE>
 FLIDE_DEV void quantize_pieces(const uint4 (&raw)[NV], int l, int nv, float sc, uint2* __restrict__ qr) {
-  auto val = [](uint32_t w, int hi) {
-    const u16 h = hi ? (u16)(w >> 16) : (u16)(w & 0xffff);
-    return BF16 ? bf16_to_f32(h) : f16_to_f32(h);
-  };
   const float rinv = 1.0f / sc, nrinv = -rinv;
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
     const int c = l + v * 64;
     if (c >= nv) continue;
-    const uint32_t w[4] = {raw[v].x, raw[v].y, raw[v].z, raw[v].w};
-    float t[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float xv = val(w[i >> 1], i & 1);
-      t[i] = FINITE ? div_markstein(xv, sc, rinv, nrinv) : xv / sc;
-      t[i] = fminf(fmaxf(t[i], -448.0f), 448.0f);
-    }
-    // gfx950's packed float32 -> OCP e4m3fn conversion (round to nearest even); on clamped inputs it
-    // gives f32_to_e4m3fn's bytes exactly (checked on every code, every tie and its neighbours)
-    uint32_t lo = __builtin_amdgcn_cvt_pk_fp8_f32(t[0], t[1], 0u, false);
-    lo = __builtin_amdgcn_cvt_pk_fp8_f32(t[2], t[3], lo, true);
-    uint32_t hi = __builtin_amdgcn_cvt_pk_fp8_f32(t[4], t[5], 0u, false);
-    hi = __builtin_amdgcn_cvt_pk_fp8_f32(t[6], t[7], hi, true);
-    qr[c] = make_uint2(lo, hi);
+    qr[c] = quantize_piece8<BF16, FINITE>(raw[v], sc, rinv, nrinv);
   }
 }
 
@@ -466,14 +434,7 @@ __global__ __launch_bounds__(RW_THREADS) void quantize_rows_vec_kernel(const u16
     raw[v] = c < nv ? xr[c] : make_uint4(0, 0, 0, 0);
   }
 #pragma unroll
-  for (int v = 0; v < NV; ++v) {
-    const uint32_t w[4] = {raw[v].x, raw[v].y, raw[v].z, raw[v].w};
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const u16 h = (i & 1) ? (u16)(w[i >> 1] >> 16) : (u16)(w[i >> 1] & 0xffff);
-      amax = fmaxf(amax, fabsf(BF16 ? bf16_to_f32(h) : f16_to_f32(h)));
-    }
-  }
+  for (int v = 0; v < NV; ++v) amax = piece8_amax<BF16>(raw[v], amax);
   // every lane holds the row's amax after the reduction; taking lane 0's makes the branch below uniform
   amax = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(wave_max(amax))));
   const float sc = fmaxf(amax, 1e-12f) * (1.0f / 448.0f);
