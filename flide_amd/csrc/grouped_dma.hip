@@ -28,9 +28,15 @@
 namespace {
 using namespace grouped_detail;
 
+//
+// NLD > 0 splits the roles: the WAVES_M x WAVES_N compute waves only read LDS, issue MFMAs and run the
+// epilogue, and NLD loader waves only issue the stage ring's loads and wait for them (a wave's vmcnt counts
+// its own loads, so no compute wave ever waits on a load). The per-stage barrier then publishes a stage
+// the loaders waited for and frees the slot the compute waves read last. The float8 gated bm-128 product
+// at 4096 tokens: 256 -> 241 us; 16-bit products gain nothing or lose (the 16-bit down product 4%).
 template <typename T, typename OutT, int ACT, int BM, int BN, int WAVES_M, int WAVES_N, int NS, int ROWB, int OCC,
-          int XCD_CHUNK_BLOCKS, bool NTW>
-__global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void grouped_dma(GroupArgs p) {
+          int XCD_CHUNK_BLOCKS, bool NTW, int NLD = 0>
+__global__ __launch_bounds__((WAVES_M * WAVES_N + NLD) * 64, OCC) void grouped_dma(GroupArgs p) {
   constexpr bool FP8 = std::is_same<T, Fp8Tag>::value;
   constexpr int EB = DmaElem<T>::BYTES;
   constexpr int KS = ROWB / EB;                // K values per stage
@@ -38,10 +44,12 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void grouped_dma(Group
   constexpr int RPI = 64 / CPR;                // rows one 1 KB load instruction fills
   constexpr int STEPS = FP8 ? 1 : ROWB / 64;   // MFMA K steps per stage
   constexpr int A_BYTES = BM * ROWB, B_BYTES = BN * ROWB, STAGE = A_BYTES + B_BYTES;
-  constexpr int NW = WAVES_M * WAVES_N;                      // waves per workgroup
-  constexpr int LA = BM / (NW * RPI), LB = BN / (NW * RPI);  // 1 KB loads per wave per stage
+  constexpr int NW = WAVES_M * WAVES_N;                      // compute waves per workgroup
+  constexpr int NLW = NLD > 0 ? NLD : NW;                    // waves that issue loads
+  constexpr int LA = BM / (NLW * RPI), LB = BN / (NLW * RPI);  // 1 KB loads per loading wave per stage
   static_assert(!FP8 || ROWB == 128, "float8 stages hold one 128-wide MFMA step");
-  static_assert(BM % (NW * RPI) == 0 && BN % (NW * RPI) == 0, "tile rows split over the waves");
+  static_assert(BM % (NLW * RPI) == 0 && BN % (NLW * RPI) == 0, "tile rows split over the loading waves");
+  static_assert(NLD == 0 || BM >= 64, "split roles only for the prefill tiles");
   constexpr int L = LA + LB;
   constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
   constexpr int FM = WM / 16, FN = WN / 16;
@@ -62,6 +70,8 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void grouped_dma(Group
 
   const int tid = threadIdx.x, l = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform, in an SGPR
+  const bool loads = NLD == 0 || wave >= NW;                   // this wave issues loads
+  const int lw = NLD > 0 ? wave - NW : wave;                   // its index among the loading waves
   // Workgroup b runs on XCD b % 8.
   int pm, pn;
   if constexpr (BM >= 64) {
@@ -123,7 +133,7 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void grouped_dma(Group
   uint32_t b_off32[LB];
 #pragma unroll
   for (int i = 0; i < LB; ++i) {
-    const int row = (wave * LB + i) * RPI + l / CPR;
+    const int row = (lw * LB + i) * RPI + l / CPR;
     long long n;
     if constexpr (ACT == ACT_NONE) {
       n = (long long)pn * BN + row;
@@ -139,17 +149,17 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void grouped_dma(Group
   // first NS - 1 stages go in flight before the block's pairs are read (their activation parts follow
   // in the K loop's prologue, which then waits for both): the workgroup's start-up keeps the memory
   // pipe busy (the plain product at 8192 tokens 1.5% faster, no change elsewhere).
-  {
+  if (loads) {
     char* const slots[4] = {lds0, lds1, lds2, lds3};
 #pragma unroll
     for (int st = 0; st < NS - 1; ++st) {
       FLIDE_LDS_AS char* sb = (FLIDE_LDS_AS char*)slots[st];
 #pragma unroll
       for (int i = 0; i < LB; ++i)
-        dma16b<NTW ? 2 : 0>(rsB, b_off32[i], (uint32_t)(st * KS * EB), sb + A_BYTES + (wave * LB + i) * 1024);
+        dma16b<NTW ? 2 : 0>(rsB, b_off32[i], (uint32_t)(st * KS * EB), sb + A_BYTES + (lw * LB + i) * 1024);
     }
   }
-  for (int r = tid; r < BM; r += NW * 64) {
+  for (int r = tid; r < BM; r += (NW + NLD) * 64) {
     const int pair = p.rows[pm * BM + r];
     s_pairs[r] = pair;
     if constexpr (FP8) {
@@ -169,10 +179,54 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void grouped_dma(Group
   uint32_t a_off32[LA];
 #pragma unroll
   for (int i = 0; i < LA; ++i) {
-    const int row = (wave * LA + i) * RPI + l / CPR;
+    const int row = (lw * LA + i) * RPI + l / CPR;
     const int pair = s_pairs[row];
     const long long src = pair < p.n_pairs ? (p.by_token ? pair / p.topk : pair) : 0;
     a_off32[i] = (uint32_t)((src * p.sa + kc) * EB);
+  }
+  if constexpr (NLD > 0) {
+    if (wave >= NW) {   // loader waves: the stage ring's loads, one barrier per stage
+      const int nk = (K + KS - 1) / KS, nfull = K / KS;
+      auto slot_at = [&](int kt) -> char* {
+        const int sl = kt % NS;
+        return sl == 0 ? lds0 : sl == 1 ? lds1 : sl == 2 ? lds2 : lds3;
+      };
+      auto issue = [&](int kt) {
+        FLIDE_LDS_AS char* sb = (FLIDE_LDS_AS char*)slot_at(kt);
+        if (kt < nfull) {
+          const uint32_t kb = (uint32_t)(kt * KS * EB);
+#pragma unroll
+          for (int i = 0; i < LA; ++i) dma16b<0>(rsA, a_off32[i], kb, sb + (lw * LA + i) * 1024);
+#pragma unroll
+          for (int i = 0; i < LB; ++i) dma16b<NTW ? 2 : 0>(rsB, b_off32[i], kb, sb + A_BYTES + (lw * LB + i) * 1024);
+        } else {   // the partial last stage: chunks past K read a 16-byte block of zeros
+          const long long kb = (long long)kt * KS * EB;
+          const bool in = kt * KS + kc < K;
+#pragma unroll
+          for (int i = 0; i < LA; ++i)
+            dma16(in ? (const void*)(A + kb + a_off32[i]) : (const void*)g_zero16, sb + (lw * LA + i) * 1024);
+#pragma unroll
+          for (int i = 0; i < LB; ++i)
+            dma16w<NTW>(in ? (const void*)(B + kb + b_off32[i]) : (const void*)g_zero16,
+                        sb + A_BYTES + (lw * LB + i) * 1024);
+        }
+      };
+      // the weight parts of stages 0 .. NS - 2 are in flight already (the host guarantees NS - 1 full stages)
+#pragma unroll
+      for (int st = 0; st < NS - 1; ++st) {
+        FLIDE_LDS_AS char* sb = (FLIDE_LDS_AS char*)slot_at(st);
+#pragma unroll
+        for (int i = 0; i < LA; ++i) dma16b<0>(rsA, a_off32[i], (uint32_t)(st * KS * EB), sb + (lw * LA + i) * 1024);
+      }
+      wait_vmcnt<0>();
+      for (int kt = 0; kt < nk; ++kt) {
+        wait_stage<NS, L>(min(NS - 2, nk - 1 - kt));
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if (kt + NS - 1 < nk) issue(kt + NS - 1);
+      }
+      return;
+    }
   }
   const int wm = wave % WAVES_M, wn = wave / WAVES_M;
   const int r = l & 15, g = l >> 4;
@@ -227,9 +281,9 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void grouped_dma(Group
       FLIDE_LDS_AS char* sb = (FLIDE_LDS_AS char*)slot_ptr(slot);
       const uint32_t kb = (uint32_t)(kt * KS * EB);
 #pragma unroll
-      for (int i = 0; i < LA; ++i) dma16b<0>(rsA, a_off32[i], kb, sb + (wave * LA + i) * 1024);
+      for (int i = 0; i < LA; ++i) dma16b<0>(rsA, a_off32[i], kb, sb + (lw * LA + i) * 1024);
 #pragma unroll
-      for (int i = 0; i < LB; ++i) dma16b<NTW ? 2 : 0>(rsB, b_off32[i], kb, sb + A_BYTES + (wave * LB + i) * 1024);
+      for (int i = 0; i < LB; ++i) dma16b<NTW ? 2 : 0>(rsB, b_off32[i], kb, sb + A_BYTES + (lw * LB + i) * 1024);
     };
     // the partial last stage (K % KS != 0): chunks past K read a 16-byte block of zeros
     auto issue_tail = [&](int kt, int slot) {
@@ -239,11 +293,11 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void grouped_dma(Group
       const bool in = k0 + kc < K;
 #pragma unroll
       for (int i = 0; i < LA; ++i)
-        dma16(in ? (const void*)(A + kb + a_off32[i]) : (const void*)g_zero16, sb + (wave * LA + i) * 1024);
+        dma16(in ? (const void*)(A + kb + a_off32[i]) : (const void*)g_zero16, sb + (lw * LA + i) * 1024);
 #pragma unroll
       for (int i = 0; i < LB; ++i)
         dma16w<NTW>(in ? (const void*)(B + kb + b_off32[i]) : (const void*)g_zero16,
-              sb + A_BYTES + (wave * LB + i) * 1024);
+              sb + A_BYTES + (lw * LB + i) * 1024);
     };
     auto compute = [&](int slot) {
       const char* sbase = slot_ptr(slot);
@@ -283,6 +337,17 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void grouped_dma(Group
       }
     };
     const int nfull = K / KS;
+    if constexpr (NLD > 0) {   // compute waves of the split roles: barrier, then the stage's reads and MFMAs
+      int slot = 0;
+      for (int kt = 0; kt < nk; ++kt) {
+        ring_barrier();
+        asm volatile("" ::: "memory");
+        compute(slot);
+        if (++slot == NS) slot = 0;
+      }
+      (void)nfull;
+      return;
+    }
     // prologue: the host guarantees NS - 1 full stages, so these loads are unconditional (a conditional
     // load here would again make the wait-count pass conservative at the loop header); the weight parts
     // went out first, so the stage counts of wait_stage do not hold until everything has landed
@@ -290,7 +355,7 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void grouped_dma(Group
     for (int st = 0; st < NS - 1; ++st) {   // activation parts; the weight parts are in flight already
       FLIDE_LDS_AS char* sb = (FLIDE_LDS_AS char*)slot_ptr(st);
 #pragma unroll
-      for (int i = 0; i < LA; ++i) dma16b<0>(rsA, a_off32[i], (uint32_t)(st * KS * EB), sb + (wave * LA + i) * 1024);
+      for (int i = 0; i < LA; ++i) dma16b<0>(rsA, a_off32[i], (uint32_t)(st * KS * EB), sb + (lw * LA + i) * 1024);
     }
     wait_vmcnt<0>();
     // steady state: stage kt computes while stages kt+1 .. kt+NS-1 load; every stage it issues is full
@@ -697,7 +762,8 @@ int launch_fp8_resident(GroupArgs& p, hipStream_t st) {
 //     workgroups per CU); bm 128 in 8-wave workgroups: the plain (down) product 64 x 32 per wave, 2
 //     stages (375 -> 290 us at 4096 tokens; with K <= 768 grouped_fp8_resident replaces it, 180 us),
 //     the gated (gate/up) product 64 x 64 per wave with BN = 256
-//     and 3 stages (144 KB; 5-10% faster than 2 x 2 waves of BN 128 at 4096-16384 tokens); bm 256:
+//     and 3 stages (144 KB; 5-10% faster than 2 x 2 waves of BN 128 at 4096-16384 tokens), its loads
+//     issued by 4 more waves (split roles: 256 -> 241 us at 4096 tokens); bm 256:
 //     2 stages = 128 KB
 //  bm 32 (decode): 128-byte stage rows, 3 stages. 16-bit: BN = 64 (gated 2 x 2 waves, plain 1 x 4),
 //     36 KB, three workgroups per CU; float8: 1 x 4 waves, BN = 128, 60 KB. Weight-streaming bound:
@@ -707,7 +773,7 @@ int launch_fp8_resident(GroupArgs& p, hipStream_t st) {
 constexpr int DMA_BN = 256;
 
 template <typename T, typename OutT, int ACT, int BM, int WM_, int WN_, int NS, int ROWB, int OCC, int XB,
-          int BN = DMA_BN>
+          int BN = DMA_BN, int NLD = 0>
 int launch_one(GroupArgs& p, hipStream_t st) {
   constexpr int KS = ROWB / DmaElem<T>::BYTES;
   if (p.K < (NS - 1) * KS) return FLIDE_MOE_ERR_TILE;   // the ring needs NS - 1 full stages
@@ -719,7 +785,7 @@ int launch_one(GroupArgs& p, hipStream_t st) {
   // decode tiles: whole XCD chunks; prefill tiles: eight equal ranges of the static item count (each
   // XCD's range of the items in use is at most that long)
   const int round = BM >= 64 ? 8 : 8 * p.ntn * XB;
-  dim3 grid((items + round - 1) / round * round), block(WM_ * WN_ * 64);
+  dim3 grid((items + round - 1) / round * round), block((WM_ * WN_ + NLD) * 64);
   // Non-temporal weight loads (dma16w / dma16b<2>) for every 32-row (decode) product and for the gated products of
   // larger tiles while padding fills at least half the blocks (most experts then hold one block, so each
   // weight tile is read once); the plain (down) products of larger tiles measured slower with them. Only
@@ -732,11 +798,11 @@ int launch_one(GroupArgs& p, hipStream_t st) {
   else if constexpr (ACT != ACT_NONE) nt = lines && 2LL * p.n_pairs <= (long long)p.nbm * BM;
   if constexpr (BM == 32 || ACT != ACT_NONE) {
     if (nt) {
-      grouped_dma<T, OutT, ACT, BM, BN, WM_, WN_, NS, ROWB, OCC, XB, true><<<grid, block, 0, st>>>(p);
+      grouped_dma<T, OutT, ACT, BM, BN, WM_, WN_, NS, ROWB, OCC, XB, true, NLD><<<grid, block, 0, st>>>(p);
       return FLIDE_MOE_OK;
     }
   }
-  grouped_dma<T, OutT, ACT, BM, BN, WM_, WN_, NS, ROWB, OCC, XB, false><<<grid, block, 0, st>>>(p);
+  grouped_dma<T, OutT, ACT, BM, BN, WM_, WN_, NS, ROWB, OCC, XB, false, NLD><<<grid, block, 0, st>>>(p);
   return FLIDE_MOE_OK;
 }
 
@@ -751,7 +817,7 @@ int launch_dma(GroupArgs& p, int bm, hipStream_t st) {
         if (launch_fp8_resident<OutT>(p, st) == FLIDE_MOE_OK) return FLIDE_MOE_OK;
         return launch_one<T, OutT, ACT, 128, 2, 4, 2, 128, 2, 4, 128>(p, st);
       }
-      else return launch_one<T, OutT, ACT, 128, 2, 4, 3, 128, 1, 4, 256>(p, st);
+      else return launch_one<T, OutT, ACT, 128, 2, 4, 3, 128, 1, 4, 256, 4>(p, st);   // + 4 loader waves
     }
     if (bm == 64) return launch_one<T, OutT, ACT, 64, 1, 4, 2, 128, 2, 8, 128>(p, st);
   } else {
