@@ -707,15 +707,18 @@ def test_load_experts_fp8(tmp_path):
     assert_close(np32(y), ref, REL_FP8, "experts from a float8 checkpoint")
 
 
+@pytest.mark.parametrize("T", [48, 2100])
 @pytest.mark.parametrize("fp8", [False, True])
-def test_graph_replays_match_eager(fp8):
+def test_graph_replays_match_eager(fp8, T):
     """The Gemma layer captured once into a HIP graph (fused router_norm -> route -> experts ->
     combine_norm_sandwich), replayed three times on new inputs written between replays by eager work: every
-    replay gives the bits of an eager run on the same inputs."""
-    print(f"graph replays fp8={fp8}", flush=True)
+    replay gives the bits of an eager run on the same inputs. 48 tokens run the decode tiles, 2100 tokens
+    (8400 pairs) the bm-128 prefill kernels (for float8 gate/up, the split-role form)."""
+    print(f"graph replays fp8={fp8} T={T}", flush=True)
     moe = _moe()
     g = torch.Generator().manual_seed(41)
-    T, H, E, k, I, eps = 48, 512, 16, 4, 128, 1e-6
+    H, E, k, I, eps = 512, 16, 4, 128, 1e-6
+    assert T < 100 or moe.tile(T * k, fp8)[0] == 128
     bf = torch.bfloat16
     w = {"experts": (torch.randn(E, 2 * I, H, generator=g) * 0.05).to(bf).to(DEV),
          "experts_down": (torch.randn(E, H, I, generator=g) * 0.05).to(bf).to(DEV), "inter": I, "topk": k}
