@@ -11,6 +11,7 @@
 //                the block -> expert map and the counts (and `used` with the last expert).
 // The result is the reference's layout exactly: per expert its pairs in ascending pair order, then the
 // sentinel n up to a multiple of bm.
+#include "quantize.hpp"
 #include "routing.hpp"
 
 namespace {
@@ -36,20 +37,17 @@ __global__ __launch_bounds__(ALIGN_THREADS) void align_count(const int* __restri
   for (int e = threadIdx.x; e < E; e += ALIGN_THREADS) hist[(long long)blockIdx.x * E + e] = h[e];
 }
 
-__global__ __launch_bounds__(ALIGN_THREADS) void align_place(const int* __restrict__ ids, int n, int E,
-                                                             int bm, int nchunks,
-                                                             const int* __restrict__ hist,
-                                                             int* __restrict__ rows,
-                                                             int* __restrict__ blocks,
-                                                             int* __restrict__ used,
-                                                             int* __restrict__ counts) {
+// Chunk c's placement by one workgroup of ALIGN_THREADS (the body of align_place).
+FLIDE_DEV void align_place_chunk(int c, const int* __restrict__ ids, int n, int E, int bm, int nchunks,
+                                 const int* __restrict__ hist, int* __restrict__ rows, int* __restrict__ blocks,
+                                 int* __restrict__ used, int* __restrict__ counts) {
   constexpr int PL = ALIGN_PER_WAVE / 64;   // pairs per lane
   __shared__ int start[ALIGN_MAX_E];    // padded start of each expert's segment
   __shared__ int before[ALIGN_MAX_E];   // this expert's pairs in earlier chunks
   __shared__ int cnt[ALIGN_MAX_E];      // total pairs per expert
   __shared__ int wcnt[ALIGN_WAVES][ALIGN_MAX_E];   // per wave: its pairs per expert, then its base
   __shared__ int scan_tmp[ALIGN_WAVES];
-  const int c = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, l = tid & 63;
+  const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63;
   // the wave's pairs [wbase, wbase + 256), 4 per lane in 64-pair groups, loaded once and held in registers
   const int wbase = c * ALIGN_CHUNK + wave * ALIGN_PER_WAVE;
   int e_g[PL];
@@ -165,6 +163,13 @@ __global__ __launch_bounds__(ALIGN_THREADS) void align_place(const int* __restri
   }
 }
 
+__global__ __launch_bounds__(ALIGN_THREADS) void align_place(const int* __restrict__ ids, int n, int E, int bm,
+                                                             int nchunks, const int* __restrict__ hist,
+                                                             int* __restrict__ rows, int* __restrict__ blocks,
+                                                             int* __restrict__ used, int* __restrict__ counts) {
+  align_place_chunk(blockIdx.x, ids, n, E, bm, nchunks, hist, rows, blocks, used, counts);
+}
+
 // Up to ALIGN_FUSED_MAX pairs: one workgroup of 8 waves, one pass over the ids. Wave w owns the pairs
 // [w * wper, (w + 1) * wper), up to 8 per lane in 64-pair groups, held in registers from one load.
 //   1. each group's lanes with the same expert find each other with ballots; the lowest one adds the
@@ -182,9 +187,8 @@ constexpr int ALIGN1_THREADS = ALIGN1_WAVES * 64;
 constexpr int ALIGN1_PER_LANE = ALIGN_FUSED_MAX / ALIGN1_THREADS;
 constexpr int ALIGN1_MAX_BLOCKS = ALIGN_FUSED_MAX + ALIGN_MAX_E;   // >= ceil((n + E (bm - 1)) / bm)
 
-__global__ __launch_bounds__(ALIGN1_THREADS) void align_one(const int* __restrict__ ids, int n, int E, int bm,
-                                                            int* __restrict__ rows, int* __restrict__ blocks,
-                                                            int* __restrict__ used, int* __restrict__ counts) {
+FLIDE_DEV void align_one_body(const int* __restrict__ ids, int n, int E, int bm, int* __restrict__ rows,
+                              int* __restrict__ blocks, int* __restrict__ used, int* __restrict__ counts) {
   __shared__ int wcnt[ALIGN1_WAVES][ALIGN_MAX_E];   // per wave: pairs per expert, then its base
   __shared__ int start[ALIGN_MAX_E], cnt[ALIGN_MAX_E];
   __shared__ int bexp[ALIGN1_MAX_BLOCKS];
@@ -292,6 +296,44 @@ __global__ __launch_bounds__(ALIGN1_THREADS) void align_one(const int* __restric
   for (int b = tid; b < nb; b += ALIGN1_THREADS) blocks[b] = bexp[b];
 }
 
+__global__ __launch_bounds__(ALIGN1_THREADS) void align_one(const int* __restrict__ ids, int n, int E, int bm,
+                                                            int* __restrict__ rows, int* __restrict__ blocks,
+                                                            int* __restrict__ used, int* __restrict__ counts) {
+  align_one_body(ids, n, E, bm, rows, blocks, used, counts);
+}
+
+// The experts call's float8 form: the placement launch's spare workgroups quantize the token rows x [M, K]
+// (quant::quantize_row16, one wave per row), which do not depend on the placement; one launch less and the
+// two overlap. Workgroups below `nplace` place pairs, the others quantize ROWS rows each.
+template <int NV, bool BF16>
+__global__ __launch_bounds__(ALIGN_THREADS) void align_place_quant(const int* __restrict__ ids, int n, int E, int bm,
+                                                                   int nchunks, const int* __restrict__ hist,
+                                                                   int* __restrict__ rows, int* __restrict__ blocks,
+                                                                   int* __restrict__ used, const u16* __restrict__ x,
+                                                                   long long sx, int K, int M, u8* __restrict__ q,
+                                                                   long long sq, float* __restrict__ s) {
+  if ((int)blockIdx.x < nchunks) {
+    align_place_chunk(blockIdx.x, ids, n, E, bm, nchunks, hist, rows, blocks, used, nullptr);
+    return;
+  }
+  const long long row = (long long)(blockIdx.x - nchunks) * (ALIGN_THREADS / 64) + (threadIdx.x >> 6);
+  if (row < M) quant::quantize_row16<NV, BF16>(x, sx, K, row, q, sq, s);
+}
+
+template <int NV, bool BF16>
+__global__ __launch_bounds__(ALIGN1_THREADS) void align_one_quant(const int* __restrict__ ids, int n, int E, int bm,
+                                                                  int* __restrict__ rows, int* __restrict__ blocks,
+                                                                  int* __restrict__ used, const u16* __restrict__ x,
+                                                                  long long sx, int K, int M, u8* __restrict__ q,
+                                                                  long long sq, float* __restrict__ s) {
+  if (blockIdx.x == 0) {
+    align_one_body(ids, n, E, bm, rows, blocks, used, nullptr);
+    return;
+  }
+  const long long row = (long long)(blockIdx.x - 1) * ALIGN1_WAVES + (threadIdx.x >> 6);
+  if (row < M) quant::quantize_row16<NV, BF16>(x, sx, K, row, q, sq, s);
+}
+
 }  // namespace
 
 // chunks of the two-launch path (1 when one workgroup handles every pair)
@@ -321,3 +363,42 @@ extern "C" int flide_moe_align(const int* ids, int n, int E, int bm, int* rows, 
   FLIDE_CHECK_LAUNCH();
   return FLIDE_MOE_OK;
 }
+
+namespace routing {
+
+int align_quantizing(const int* ids, int n, int E, int bm, int* rows, int* blocks, int* used, void* workspace,
+                     size_t workspace_bytes, const void* x, long long sx, int M, int K, int x_dtype, void* q,
+                     long long sq, float* s, hipStream_t st) {
+  if (n <= 0 || E <= 0 || E > ALIGN_MAX_E || bm <= 0 || M <= 0 || !quant::row16_ok(x, sx, K, x_dtype, q, sq))
+    return FLIDE_MOE_ERR_TILE;
+  if (workspace_bytes < flide_moe_align_workspace(n, E)) return FLIDE_MOE_ERR_WORKSPACE;
+  const int nchunks = align_chunks(n);
+  int* hist = (int*)workspace;
+  const bool bf = x_dtype == FLIDE_BF16;
+  const int nv = quant::row16_nv(K);
+  const u16* xx = (const u16*)x;
+  u8* qq = (u8*)q;
+#define AQ(NV)                                                                                                   \
+  do {                                                                                                           \
+    if (nchunks == 1) {                                                                                          \
+      const dim3 g(1 + (M + ALIGN1_WAVES - 1) / ALIGN1_WAVES);                                                  \
+      if (bf) align_one_quant<NV, true><<<g, ALIGN1_THREADS, 0, st>>>(ids, n, E, bm, rows, blocks, used, xx, sx, K, M, qq, sq, s); \
+      else align_one_quant<NV, false><<<g, ALIGN1_THREADS, 0, st>>>(ids, n, E, bm, rows, blocks, used, xx, sx, K, M, qq, sq, s); \
+    } else {                                                                                                     \
+      align_count<<<nchunks, ALIGN_THREADS, 0, st>>>(ids, n, E, hist);                                           \
+      const dim3 g(nchunks + (M + ALIGN_WAVES - 1) / ALIGN_WAVES);                                              \
+      if (bf) align_place_quant<NV, true><<<g, ALIGN_THREADS, 0, st>>>(ids, n, E, bm, nchunks, hist, rows, blocks, used, xx, sx, K, M, qq, sq, s); \
+      else align_place_quant<NV, false><<<g, ALIGN_THREADS, 0, st>>>(ids, n, E, bm, nchunks, hist, rows, blocks, used, xx, sx, K, M, qq, sq, s); \
+    }                                                                                                            \
+  } while (0)
+  if (nv == 1) AQ(1);
+  else if (nv == 2) AQ(2);
+  else if (nv == 4) AQ(4);
+  else if (nv == 8) AQ(8);
+  else AQ(16);
+#undef AQ
+  FLIDE_CHECK_LAUNCH();
+  return FLIDE_MOE_OK;
+}
+
+}  // namespace routing

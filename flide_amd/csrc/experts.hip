@@ -71,7 +71,8 @@ bool experts_args_ok(int T, int H, int k, int E, int I, int bm, int x_dtype, int
 // The two products on align's layout (rows, blocks, used in the workspace `ws` carved by `L`).
 int run_products(const void* x, long long sx, int x_dtype, int T, int H, const float* top, int k,
                  const void* w_gu, const void* w_d, const float* w_scale_gu, const float* w_scale_d, int E, int I,
-                 void* y, int act, int bm, int bn, char* ws, const ExpertsLayout& L, flide_stream_t stream) {
+                 void* y, int act, int bm, int bn, char* ws, const ExpertsLayout& L, bool x_quantized,
+                 flide_stream_t stream) {
   const int fp8 = w_scale_gu != nullptr;
   int* rows = (int*)(ws + L.rows);
   int* blocks = (int*)(ws + L.blocks);
@@ -92,8 +93,10 @@ int run_products(const void* x, long long sx, int x_dtype, int T, int H, const f
   float* sxs = (float*)(ws + L.sx);
   u8* qa = (u8*)(ws + L.qa);
   float* sas = (float*)(ws + L.sa);
-  rc = flide_moe_quantize_rows(x, sx, T, H, x_dtype, qx, H, sxs, stream);
-  if (rc) return rc;
+  if (!x_quantized) {
+    rc = flide_moe_quantize_rows(x, sx, T, H, x_dtype, qx, H, sxs, stream);
+    if (rc) return rc;
+  }
   rc = flide_moe_grouped_fp8(qx, H, sxs, w_gu, (long long)2 * I * H, H, w_scale_gu, 2 * I, 2 * I, H,
                              actbuf, I, x_dtype, nullptr, rows, blocks, used, n, nbm, k, 1, act, bm,
                              bn, stream);
@@ -117,11 +120,25 @@ int run_experts(const void* x, long long sx, int x_dtype, int T, int H, const fl
   if (T == 0) return FLIDE_MOE_OK;
   const ExpertsLayout L = layout(T, k, E, H, I, bm, w_scale_gu != nullptr);
   if (ws_bytes < L.total) return FLIDE_MOE_ERR_WORKSPACE;
-  int rc = flide_moe_align(ids, T * k, E, bm, (int*)(ws + L.rows), (int*)(ws + L.blocks), (int*)(ws + L.used),
-                           nullptr, ws + L.hist, L.rows - L.hist, stream);
-  if (rc) return rc;
+  int* rows = (int*)(ws + L.rows);
+  int* blocks = (int*)(ws + L.blocks);
+  int* used = (int*)(ws + L.used);
+  // float8 experts: the token rows are quantized by the placement launch's spare workgroups where the
+  // vector quantizer takes them (one launch less; the two overlap), else by their own launch below
+  bool xq = false;
+  int rc;
+  if (w_scale_gu != nullptr) {
+    rc = routing::align_quantizing(ids, T * k, E, bm, rows, blocks, used, ws + L.hist, L.rows - L.hist, x, sx, T,
+                                   H, x_dtype, ws + L.qx, H, (float*)(ws + L.sx), (hipStream_t)stream);
+    if (rc == FLIDE_MOE_OK) xq = true;
+    else if (rc != FLIDE_MOE_ERR_TILE) return rc;
+  }
+  if (!xq) {
+    rc = flide_moe_align(ids, T * k, E, bm, rows, blocks, used, nullptr, ws + L.hist, L.rows - L.hist, stream);
+    if (rc) return rc;
+  }
   return run_products(x, sx, x_dtype, T, H, top, k, w_gu, w_d, w_scale_gu, w_scale_d, E, I, y, act, bm, bn, ws,
-                      L, stream);
+                      L, xq, stream);
 }
 
 // The allocation-free entry point's scratch: one copy of this array per device, resident from module

@@ -103,4 +103,11 @@ FLIDE_DEV void route_select(const float (&v)[EPL], const float (&sc)[EPL], int E
   }
 }
 
+// The experts call's float8 form of flide_moe_align (align.hip): the same placement (counts not written),
+// with the token rows x [M, K] quantized per row into q / s by the placement launch's spare workgroups.
+// FLIDE_MOE_ERR_TILE when the rows do not suit the vector quantizer (the caller then runs the two apart).
+int align_quantizing(const int* ids, int n, int E, int bm, int* rows, int* blocks, int* used, void* workspace,
+                     size_t workspace_bytes, const void* x, long long sx, int M, int K, int x_dtype, void* q,
+                     long long sq, float* s, hipStream_t st);
+
 }  // namespace routing

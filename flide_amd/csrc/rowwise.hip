@@ -8,6 +8,7 @@
 #include <type_traits>
 
 #include "common.hpp"
+#include "quantize.hpp"
 
 namespace {
 
@@ -401,49 +402,14 @@ __global__ __launch_bounds__(RW_THREADS) void quantize_rows_kernel(const void* _
   }
 }
 
-// quantize_rows_vec_kernel's second pass: the row's pieces (already in registers) to e4m3 bytes.
-template <int NV, bool BF16, bool FINITE>
-FLIDE_DEV void quantize_pieces(const uint4 (&raw)[NV], int l, int nv, float sc, uint2* __restrict__ qr) {
-  const float rinv = 1.0f / sc, nrinv = -rinv;
-#pragma unroll
-  for (int v = 0; v < NV; ++v) {
-    const int c = l + v * 64;
-    if (c >= nv) continue;
-    qr[c] = quantize_piece8<BF16, FINITE>(raw[v], sc, rinv, nrinv);
-  }
-}
-
-// 16-bit rows, K % 8 == 0, K <= NV * 512: one wave per row (4 rows per workgroup). The row is loaded
-// once in 16-byte pieces and kept in registers between the amax and the quantization; each lane stores
-// 8 quantized bytes at a time. The same bytes as quantize_rows_kernel (its true float32 division, made
-// here by div_markstein, or by the division for a row holding an inf).
+// 16-bit rows, K % 8 == 0, K <= NV * 512: one wave per row (4 rows per workgroup), quant::quantize_row16.
 template <int NV, bool BF16>
 __global__ __launch_bounds__(RW_THREADS) void quantize_rows_vec_kernel(const u16* __restrict__ x, long long sx,
                                                                        int K, int M, u8* __restrict__ q,
                                                                        long long sq, float* __restrict__ s) {
-  const int l = threadIdx.x & 63;
   const long long row = (long long)blockIdx.x * (RW_THREADS / 64) + (threadIdx.x >> 6);
   if (row >= M) return;
-  const int nv = K / 8;
-  const uint4* xr = (const uint4*)(x + row * sx);
-  uint4 raw[NV];
-  float amax = 0.f;
-#pragma unroll
-  for (int v = 0; v < NV; ++v) {
-    const int c = l + v * 64;
-    raw[v] = c < nv ? xr[c] : make_uint4(0, 0, 0, 0);
-  }
-#pragma unroll
-  for (int v = 0; v < NV; ++v) amax = piece8_amax<BF16>(raw[v], amax);
-  // every lane holds the row's amax after the reduction; taking lane 0's makes the branch below uniform
-  amax = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(wave_max(amax))));
-  const float sc = fmaxf(amax, 1e-12f) * (1.0f / 448.0f);
-  if (l == 0) s[row] = sc;
-  uint2* qr = (uint2*)(q + row * sq);
-  if (sc < INFINITY)
-    quantize_pieces<NV, BF16, true>(raw, l, nv, sc, qr);
-  else
-    quantize_pieces<NV, BF16, false>(raw, l, nv, sc, qr);
+  quant::quantize_row16<NV, BF16>(x, sx, K, row, q, sq, s);
 }
 
 // ---------------------------------------------------------------------------------------------------
@@ -558,10 +524,8 @@ extern "C" int flide_moe_quantize_rows(const void* x, long long sx, int M, int K
   if (M < 0 || K < 0 || !dtype_ok(x_dtype)) return FLIDE_MOE_ERR_ARG;
   if (M == 0) return FLIDE_MOE_OK;
   hipStream_t st = (hipStream_t)stream;
-  const bool vec = x_dtype != FLIDE_F32 && K % 8 == 0 && K <= 16 * 512 && sx % 8 == 0 && sq % 8 == 0 &&
-                   !((uintptr_t)x & 15) && !((uintptr_t)q & 7);
-  if (vec) {
-    const int per_lane = (K / 8 + 63) / 64;
+  if (quant::row16_ok(x, sx, K, x_dtype, q, sq)) {
+    const int nv = quant::row16_nv(K);
     const dim3 grid((M + 3) / 4);
 #define QV(NV)                                                                                            \
   do {                                                                                                     \
@@ -570,10 +534,10 @@ extern "C" int flide_moe_quantize_rows(const void* x, long long sx, int M, int K
     else                                                                                                   \
       quantize_rows_vec_kernel<NV, false><<<grid, RW_THREADS, 0, st>>>((const u16*)x, sx, K, M, (u8*)q, sq, s); \
   } while (0)
-    if (per_lane <= 1) QV(1);
-    else if (per_lane <= 2) QV(2);
-    else if (per_lane <= 4) QV(4);
-    else if (per_lane <= 8) QV(8);
+    if (nv == 1) QV(1);
+    else if (nv == 2) QV(2);
+    else if (nv == 4) QV(4);
+    else if (nv == 8) QV(8);
     else QV(16);
 #undef QV
     FLIDE_CHECK_LAUNCH();

@@ -23,6 +23,12 @@ def _moe():
     return moe
 
 
+def _hip_mod():
+    from flide_amd import _hip
+
+    return _hip
+
+
 def _gelu_act(gu, n):
     from flide_amd.kernels import pointwise as pw
 
@@ -370,6 +376,34 @@ def test_experts_cfg1_shape_other_tiles():
         sub = np.random.default_rng(T).choice(T * 8, 256, replace=False)
         got, ref, _ = _experts_case(1, T=T, pairs_subset=np.sort(sub))
         assert_close(got, ref, REL_BF16, f"experts T={T}")
+
+
+@pytest.mark.parametrize("T,E,H,I,dt", [(40, 16, 2816, 704, torch.bfloat16), (700, 12, 1008, 320, torch.float16),
+                                       (1100, 16, 2816, 704, torch.bfloat16)])
+def test_experts_fp8_matches_call_sequence(T, E, H, I, dt):
+    """The FP8 experts call quantizes the token rows inside its placement launch (align_one below 4096 pairs,
+    align_place above): bit-identical to the reference's sequence align -> grouped_fp8 (gate/up, quantizing
+    x) -> grouped_fp8 (down, x weight) on the same tiles (moe.py:336-353)."""
+    print(f"experts fp8 vs call sequence T={T} E={E} H={H} I={I} {dt}", flush=True)
+    moe = _moe()
+    k = 8
+    g = torch.Generator(device=DEV).manual_seed(T + H)
+    logits = torch.randn(T, E, generator=g, device=DEV)
+    x = torch.randn(T, H, generator=g, device=DEV).to(dt)
+    q_gu, s_gu = moe.quantize_experts((torch.randn(E, 2 * I, H, generator=g, device=DEV) * 0.02).to(dt))
+    q_d, s_d = moe.quantize_experts((torch.randn(E, H, I, generator=g, device=DEV) * 0.02).to(dt))
+    top, ids = moe.route(logits, k)
+    w = {"experts": q_gu, "experts_down": q_d, "inter": I, "experts_scale": s_gu, "experts_down_scale": s_d}
+    y = moe.experts(x, w, top, ids, _gelu_act)
+    tl = moe.tile(T * k, True)
+    rows, blocks, used = moe.align(ids, E, tl[0])
+    act = torch.empty(T * k, I, dtype=dt, device=DEV)
+    moe.grouped_fp8(x, q_gu, s_gu, act, rows, blocks, used, k, True, tile=tl, act=_hip_mod().ACT_GEGLU)
+    ref = torch.full((T * k, H), float("nan"), dtype=dt, device=DEV)
+    moe.grouped_fp8(act, q_d, s_d, ref, rows, blocks, used, k, False, top.reshape(-1), tile=tl)
+    torch.cuda.synchronize()
+    assert not torch.isnan(ref.float()).any()
+    assert torch.equal(y, ref), f"{(y != ref).sum().item()} of {y.numel()} values differ"
 
 
 def test_experts_cfg3_fp8_subset():
