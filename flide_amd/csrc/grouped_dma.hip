@@ -256,6 +256,16 @@ __global__ __launch_bounds__((WAVES_M * WAVES_N + NLD) * 64, OCC) void grouped_d
   }
   auto b_off = [&](int fn, int j) { return A_BYTES + brow[fn] * ROWB + lane_off[j]; };
   const int ncols = ACT == ACT_NONE ? p.N : half;
+  // gated float8 tiles: the gate and up column scales of this lane's output columns, loaded now so that the
+  // epilogue does not start with a round trip (1 for 16-bit weights)
+  float cs_g[FN / 2 > 0 ? FN / 2 : 1], cs_u[FN / 2 > 0 ? FN / 2 : 1];
+#pragma unroll
+  for (int fn = 0; fn < FN / 2; ++fn) {
+    const int col = colbase[fn] + r;
+    const bool ok = col < half;
+    cs_g[fn] = FP8 && ACT != ACT_NONE && ok ? p.w_scale[e * p.sse + col] : (FP8 ? 0.f : 1.f);
+    cs_u[fn] = FP8 && ACT != ACT_NONE && ok ? p.w_scale[e * p.sse + col + half] : (FP8 ? 0.f : 1.f);
+  }
   const bool wave_live = __builtin_amdgcn_readfirstlane(colbase[0]) < ncols && m_live[0];   // stores anything
 
   f32x4_t acc[FM][FN];
@@ -412,10 +422,65 @@ __global__ __launch_bounds__((WAVES_M * WAVES_N + NLD) * 64, OCC) void grouped_d
     kloop(std::integral_constant<int, FM>{}, lds0, lds1, lds2, lds3);
   }
 
-  if (!wave_live) return;
-
   typedef typename std::conditional<FP8, typename OutRound<OutT>::type, T>::type RT;   // gu rounding
   const float* ws = FP8 ? p.w_scale + e * p.sse : nullptr;
+  if constexpr (BM == 128 && ACT != ACT_NONE && sizeof(typename OutTraits<OutT>::storage) == 2) {
+    // Gated bm-128 products with 16-bit outputs in rows of 16-byte pieces: the tile's BM x BN/2 activation
+    // values are staged in ring slot 0 (free once every compute wave is past the K loop), then each lane
+    // stores 8 columns of a row, so a store instruction writes whole 256-byte row segments instead of
+    // 2-byte values scattered over 4 rows (float8 gate/up at 4096 tokens 247 -> 232 us, 16-bit gate/up at
+    // 8192 tokens 655 -> 627 us, 16384 tokens on skewed routing 1219 -> 1161 us; same values)
+    if (!p.weights && ((uintptr_t)p.out & 15) == 0 && p.sc % 8 == 0) {
+      typedef typename OutTraits<OutT>::storage S;
+      constexpr int TC = BN / 2;
+      static_assert(BM * TC * 2 <= STAGE, "the staged tile fits a ring slot");
+      S* tile = (S*)lds0;
+      ring_barrier();   // every compute wave is done reading the ring (loader waves, if any, have ended)
+      if (wave_live) {
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm) {
+          if (!m_live[fm]) continue;
+          const int row0 = wm * WM + fm * 16;
+          float rs[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) rs[i] = FP8 ? s_ascale[row0 + g * 4 + i] : 1.f;
+#pragma unroll
+          for (int fn = 0; fn < FN / 2; ++fn) {
+            const int col = colbase[fn] + r;
+            const int lc = col - pn * TC;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {   // the values store_frag computes, in the same order
+              const float gg = round_in<RT>(acc[fm][fn][i] * rs[i] * cs_g[fn]);
+              const float uu = round_in<RT>(acc[fm][fn + FN / 2][i] * rs[i] * cs_u[fn]);
+              tile[(row0 + g * 4 + i) * TC + lc] = OutTraits<OutT>::conv(act_f32<ACT>(gg, uu));
+            }
+          }
+        }
+      }
+      ring_barrier();
+      constexpr int LPR = TC / 8;        // lanes per row, 8 columns each
+      constexpr int RPP = NW * 64 / LPR;   // rows per pass
+      const int c8 = (tid % LPR) * 8;
+      const int col0 = pn * TC + c8;
+      for (int rr = tid / LPR; rr < BM; rr += RPP) {
+        const int pair = s_pairs[rr];
+        if (pair >= p.n_pairs || col0 >= half) continue;
+        const uint4 q = *(const uint4*)(tile + rr * TC + c8);
+        S* o = (S*)p.out + (long long)pair * p.sc + col0;
+        if (col0 + 8 <= half) {
+          *(uint4*)o = q;
+        } else {
+          const S ev[8] = {(S)(q.x & 0xffff), (S)(q.x >> 16), (S)(q.y & 0xffff), (S)(q.y >> 16),
+                           (S)(q.z & 0xffff), (S)(q.z >> 16), (S)(q.w & 0xffff), (S)(q.w >> 16)};
+#pragma unroll
+          for (int j = 0; j < 7; ++j)
+            if (col0 + j < half) o[j] = ev[j];
+        }
+      }
+      return;
+    }
+  }
+  if (!wave_live) return;
 #pragma unroll
   for (int fm = 0; fm < FM; ++fm) {
     if (!m_live[fm]) continue;
@@ -447,8 +512,7 @@ __global__ __launch_bounds__((WAVES_M * WAVES_N + NLD) * 64, OCC) void grouped_d
       for (int fn = 0; fn < FN / 2; ++fn) {
         const int col = colbase[fn] + r;
         const bool ok = col < half;
-        store_frag<OutT, ACT, RT>(p, s_pairs, row0, col, acc[fm][fn], acc[fm][fn + FN / 2],
-                                  FP8 ? (ok ? ws[col] : 0.f) : 1.f, FP8 ? (ok ? ws[col + half] : 0.f) : 1.f,
+        store_frag<OutT, ACT, RT>(p, s_pairs, row0, col, acc[fm][fn], acc[fm][fn + FN / 2], cs_g[fn], cs_u[fn],
                                   rs, ok);
       }
     }
