@@ -253,14 +253,17 @@ FLIDE_DEV f32x4_t mfma_fp8(const i32x8_t& a, const i32x8_t& b, const f32x4_t& c)
 // ---------------------------------------------------------------------------------------------------
 // activations between the two grouped products (flide/kernels/pointwise.py:52-59,248-257)
 // ---------------------------------------------------------------------------------------------------
-// GELU-tanh(a) * b as 0.5 a (2 - 2 / (1 + e^{2z})), z = sqrt(2/pi) (a + 0.044715 a^3)
+// GELU-tanh(a) * b. 0.5 a (1 + tanh z) with z = sqrt(2/pi) (a + 0.044715 a^3) equals a / (1 + e^{-2z}),
+// evaluated with the hardware reciprocal (v_rcp_f32, 1 ulp) instead of an IEEE division (about ten
+// instructions with its scaling and fix-up): an epilogue evaluates this for every output of a gated tile.
+// Large negative a: e^{-2z} overflows to inf, the reciprocal gives 0 and so does the product.
 FLIDE_DEV float geglu_f32(float a, float b) {
-  float z = 0.7978845608028654f * (a + 0.044715f * a * a * a);
-  float g = 0.5f * a * (2.0f - 2.0f / (1.0f + __expf(2.0f * z)));
-  return g * b;
+  const float y = -1.5957691216057308f * (a + 0.044715f * a * a * a);   // -2z
+  return a * __builtin_amdgcn_rcpf(1.0f + __expf(y)) * b;
 }
 
-FLIDE_DEV float swiglu_f32(float a, float b) { return a / (1.0f + __expf(-a)) * b; }
+// SiLU(a) * b = a / (1 + e^{-a}) * b, with the same reciprocal
+FLIDE_DEV float swiglu_f32(float a, float b) { return a * __builtin_amdgcn_rcpf(1.0f + __expf(-a)) * b; }
 
 enum { ACT_NONE = 0, ACT_GEGLU = 1, ACT_SWIGLU = 2 };
 

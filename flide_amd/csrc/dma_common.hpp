@@ -22,6 +22,11 @@ FLIDE_DEV void dma16(const void* src, FLIDE_LDS_AS void* dst) {
   __builtin_amdgcn_global_load_lds((const FLIDE_GLOBAL_AS void*)src, dst, 16, 0, 0);
 }
 
+// 4 bytes per lane (global_load_lds_dword): lane l's value lands at dst + 4 l
+FLIDE_DEV void dma4(const void* src, FLIDE_LDS_AS void* dst) {
+  __builtin_amdgcn_global_load_lds((const FLIDE_GLOBAL_AS void*)src, dst, 4, 0, 0);
+}
+
 // The same load through a raw buffer resource (buffer_load_dwordx4 ... lds): the per-lane offset is a
 // 32-bit VGPR and the stage's K offset an SGPR, so a full stage needs no per-lane 64-bit address
 // arithmetic and each load keeps one VGPR instead of two (the 16-bit gated product at 8192 tokens 4%
@@ -108,6 +113,29 @@ FLIDE_DEV int expert_end_block(const int* blocks, int blk, int e, int nused, int
     if (m) return base + __builtin_ctzll(m);
     base += 64;
   }
+}
+
+// The expert e = blocks[blk] and the run [first, end) of its blocks. One pair of loads covers blocks
+// blk - 63 .. blk + 63, so a run of up to 64 blocks on either side costs one round trip (the searches
+// above need one for blocks[blk] and one more each); longer runs continue with those searches.
+FLIDE_DEV int expert_run(const int* blocks, int blk, int nused, int l, int& first, int& end) {
+  const int lo_idx = blk - 63 + l, hi_idx = blk + l;
+  const int lo = lo_idx >= 0 ? blocks[lo_idx] : -1;
+  const int hi = hi_idx < nused ? blocks[hi_idx] : -1;
+  const int e = __builtin_amdgcn_readfirstlane(hi);   // lane 0 read blocks[blk]
+  const unsigned long long ml = __ballot(lo != e), mh = __ballot(hi != e);
+  first = ml ? blk - 63 + (63 - __builtin_clzll(ml)) + 1 : expert_first_block(blocks, blk - 64, e, l);
+  end = mh ? blk + __builtin_ctzll(mh) : expert_end_block(blocks, blk + 64, e, nused, l);
+  return e;
+}
+
+// Workgroup barrier for LDS data only: waits for this wave's LDS accesses but not for its global loads
+// (loads into the stage ring stay in flight), and keeps the compiler from moving memory accesses across.
+FLIDE_DEV void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
 }
 
 }  // namespace

@@ -74,6 +74,7 @@ __global__ __launch_bounds__((WAVES_M * WAVES_N + NLD) * 64, OCC) void grouped_d
   const int lw = NLD > 0 ? wave - NW : wave;                   // its index among the loading waves
   // Workgroup b runs on XCD b % 8.
   int pm, pn;
+  long long e;   // the block's expert
   if constexpr (BM >= 64) {
     // Prefill tiles: the items (block, column tile) in use, ordered by expert, are split into 8
     // contiguous ranges, range x for the workgroups of XCD x. An expert's blocks and all its column
@@ -87,12 +88,13 @@ __global__ __launch_bounds__((WAVES_M * WAVES_N + NLD) * 64, OCC) void grouped_d
     const int x = blockIdx.x & 7;
     const long long it = R * x / 8 + (blockIdx.x >> 3);
     if (it >= R * (x + 1) / 8) return;
-    const int blk = (int)(it / p.ntn);
-    const int ex = p.blocks[blk];
-    const int s0 = __builtin_amdgcn_readfirstlane(expert_first_block(p.blocks, blk, ex, l));
+    const int blk = (int)(it / p.ntn);   // a block of the item's expert
+    int s0, s1;
+    e = expert_run(p.blocks, blk, nused, l, s0, s1);
+    s0 = __builtin_amdgcn_readfirstlane(s0);
     const int local = (int)(it - (long long)s0 * p.ntn);
     if constexpr (ACT != ACT_NONE) {
-      const int nb = __builtin_amdgcn_readfirstlane(expert_end_block(p.blocks, blk, ex, nused, l)) - s0;
+      const int nb = __builtin_amdgcn_readfirstlane(s1) - s0;
       pn = local / nb;
       pm = s0 + local % nb;
     } else {
@@ -119,8 +121,8 @@ __global__ __launch_bounds__((WAVES_M * WAVES_N + NLD) * 64, OCC) void grouped_d
       pn = widx % p.ntn;
     }
     if (pm >= p.nbm || pm * BM >= *p.used) return;
+    e = __builtin_amdgcn_readfirstlane(p.blocks[pm]);
   }
-  const long long e = __builtin_amdgcn_readfirstlane(p.blocks[pm]);
   const int K = p.K;
   const int half = p.N / 2;
   const char* A = (const char*)p.a;
@@ -159,16 +161,23 @@ __global__ __launch_bounds__((WAVES_M * WAVES_N + NLD) * 64, OCC) void grouped_d
         dma16b<NTW ? 2 : 0>(rsB, b_off32[i], (uint32_t)(st * KS * EB), sb + A_BYTES + (lw * LB + i) * 1024);
     }
   }
+  // Float8 split-role tiles: the rows' activation scales are needed only by the epilogue, so their loads
+  // (which need the pair loads) go straight to LDS and stay in flight through the K loop; the compute
+  // waves wait for them after it. One row per thread (BM <= the workgroup's threads, rows in whole waves).
+  constexpr bool DEFER_SCALE = FP8 && NLD > 0 && (NW + NLD) * 64 >= BM && BM % 64 == 0;
   for (int r = tid; r < BM; r += (NW + NLD) * 64) {
     const int pair = p.rows[pm * BM + r];
     s_pairs[r] = pair;
     if constexpr (FP8) {
       const long long src = p.by_token ? pair / p.topk : pair;
-      s_ascale[r] = pair < p.n_pairs ? p.a_scale[src] : 0.f;
+      if constexpr (DEFER_SCALE)
+        dma4(pair < p.n_pairs ? (const void*)(p.a_scale + src) : (const void*)g_zero16,
+             (FLIDE_LDS_AS char*)s_ascale + (r & ~63) * 4);
+      else s_ascale[r] = pair < p.n_pairs ? p.a_scale[src] : 0.f;
     }
     if constexpr (ACT == ACT_NONE) s_wt[r] = p.weights && pair < p.n_pairs ? p.weights[pair] : 1.f;
   }
-  __syncthreads();
+  lds_barrier();   // the weight loads of the first stages stay in flight
 
   // This lane's global source for each of its loads: tile row (instr * RPI + l / CPR) and logical chunk
   // c = (l % CPR) ^ swz(row). Instruction rows start at multiples of RPI, so swz(row) and therefore c
@@ -347,16 +356,75 @@ __global__ __launch_bounds__((WAVES_M * WAVES_N + NLD) * 64, OCC) void grouped_d
       }
     };
     const int nfull = K / KS;
-    if constexpr (NLD > 0) {   // compute waves of the split roles: barrier, then the stage's reads and MFMAs
-      int slot = 0;
-      for (int kt = 0; kt < nk; ++kt) {
+    if constexpr (NLD > 0) {
+      // Compute waves of the split roles. The barrier that publishes stage kt + 1 sits in the middle of
+      // stage kt's MFMAs: the fragment rows [0, H1) run first, which frees their A fragments; after the
+      // barrier those are read again from stage kt + 1 under the MFMAs of rows [H1, FMA), and the B
+      // fragments and the remaining A fragments follow. A wave thus enters every barrier with MFMA work
+      // whose operands are in registers, instead of all waves reading the stage at once behind it
+      // (compute half alone: 1474 -> 1219 cycles per float8 stage of a 128 x 256 tile; same registers).
+      // A fragment is two 16-byte LDS reads: lo/hi K halves of one float8 step, or two 16-bit steps.
+      static_assert(FP8 || STEPS == 2, "two 16-byte reads per fragment");
+      (void)nfull;
+      if constexpr (FMA == 0) {
+        for (int kt = 0; kt < nk; ++kt) ring_barrier();
+        return;
+      } else {
+        constexpr int H1 = FMA < 2 ? FMA : 2;
+        u32x4_t af[FMA][2], bfr[FN][2];
+        auto read_a = [&](const char* sb, int fm) {
+          af[fm][0] = *(const u32x4_t*)(sb + a_off(fm, 0));
+          af[fm][1] = *(const u32x4_t*)(sb + a_off(fm, 1));
+        };
+        auto read_b = [&](const char* sb, int fn) {
+          bfr[fn][0] = *(const u32x4_t*)(sb + b_off(fn, 0));
+          bfr[fn][1] = *(const u32x4_t*)(sb + b_off(fn, 1));
+        };
+        auto rows = [&](auto lo_tag, auto hi_tag) {   // the MFMAs of fragment rows [LO, HI) of one stage
+#pragma unroll
+          for (int fm = decltype(lo_tag)::value; fm < decltype(hi_tag)::value; ++fm)
+#pragma unroll
+            for (int fn = 0; fn < FN; ++fn) {
+              if constexpr (FP8) {
+                const u32x4_t *a = af[fm], *b = bfr[fn];
+                acc[fm][fn] = mfma_fp8(i32x8_t{(int)a[0][0], (int)a[0][1], (int)a[0][2], (int)a[0][3], (int)a[1][0], (int)a[1][1], (int)a[1][2], (int)a[1][3]},
+                                       i32x8_t{(int)b[0][0], (int)b[0][1], (int)b[0][2], (int)b[0][3], (int)b[1][0], (int)b[1][1], (int)b[1][2], (int)b[1][3]},
+                                       acc[fm][fn]);
+              } else {
+                acc[fm][fn] = Mfma16<T>::mma(af[fm][0], bfr[fn][0], acc[fm][fn]);
+                acc[fm][fn] = Mfma16<T>::mma(af[fm][1], bfr[fn][1], acc[fm][fn]);
+              }
+            }
+        };
+        auto read_rest = [&](const char* sb) {
+#pragma unroll
+          for (int fn = 0; fn < FN; ++fn) read_b(sb, fn);
+#pragma unroll
+          for (int fm = H1; fm < FMA; ++fm) read_a(sb, fm);
+        };
         ring_barrier();
         asm volatile("" ::: "memory");
-        compute(slot);
-        if (++slot == NS) slot = 0;
+#pragma unroll
+        for (int fm = 0; fm < H1; ++fm) read_a(slot_ptr(0), fm);
+        read_rest(slot_ptr(0));
+        int slot = 0;
+        // every iteration but the last publishes and reads the next stage (branch-free, see above)
+        for (int kt = 0; kt + 1 < nk; ++kt) {
+          const int nxt = slot + 1 == NS ? 0 : slot + 1;
+          rows(std::integral_constant<int, 0>{}, std::integral_constant<int, H1>{});
+          __builtin_amdgcn_sched_barrier(0);   // those MFMAs issue before the barrier, not after it
+          ring_barrier();
+          asm volatile("" ::: "memory");
+          const char* sb = slot_ptr(nxt);
+#pragma unroll
+          for (int fm = 0; fm < H1; ++fm) read_a(sb, fm);
+          rows(std::integral_constant<int, H1>{}, std::integral_constant<int, FMA>{});
+          read_rest(sb);
+          slot = nxt;
+        }
+        rows(std::integral_constant<int, 0>{}, std::integral_constant<int, FMA>{});
+        return;
       }
-      (void)nfull;
-      return;
     }
     // prologue: the host guarantees NS - 1 full stages, so these loads are unconditional (a conditional
     // load here would again make the wait-count pass conservative at the loop header); the weight parts
@@ -422,6 +490,10 @@ __global__ __launch_bounds__((WAVES_M * WAVES_N + NLD) * 64, OCC) void grouped_d
     kloop(std::integral_constant<int, FM>{}, lds0, lds1, lds2, lds3);
   }
 
+  if constexpr (DEFER_SCALE) {
+    wait_vmcnt<0>();
+    ring_barrier();   // the scales are in LDS, and every compute wave is done reading the ring
+  }
   typedef typename std::conditional<FP8, typename OutRound<OutT>::type, T>::type RT;   // gu rounding
   const float* ws = FP8 ? p.w_scale + e * p.sse : nullptr;
   if constexpr (BM == 128 && ACT != ACT_NONE && sizeof(typename OutTraits<OutT>::storage) == 2) {
@@ -435,7 +507,7 @@ __global__ __launch_bounds__((WAVES_M * WAVES_N + NLD) * 64, OCC) void grouped_d
       constexpr int TC = BN / 2;
       static_assert(BM * TC * 2 <= STAGE, "the staged tile fits a ring slot");
       S* tile = (S*)lds0;
-      ring_barrier();   // every compute wave is done reading the ring (loader waves, if any, have ended)
+      if constexpr (!DEFER_SCALE) ring_barrier();   // every compute wave is done reading the ring
       if (wave_live) {
 #pragma unroll
         for (int fm = 0; fm < FM; ++fm) {
