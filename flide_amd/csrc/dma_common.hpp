@@ -11,6 +11,7 @@ namespace {
 using namespace grouped_detail;
 
 __device__ __attribute__((aligned(16))) const uint32_t g_zero16[4] = {0, 0, 0, 0};
+__device__ const float g_one = 1.0f;
 
 template <int N> FLIDE_DEV void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");

@@ -161,21 +161,27 @@ __global__ __launch_bounds__((WAVES_M * WAVES_N + NLD) * 64, OCC) void grouped_d
         dma16b<NTW ? 2 : 0>(rsB, b_off32[i], (uint32_t)(st * KS * EB), sb + A_BYTES + (lw * LB + i) * 1024);
     }
   }
-  // Float8 split-role tiles: the rows' activation scales are needed only by the epilogue, so their loads
-  // (which need the pair loads) go straight to LDS and stay in flight through the K loop; the compute
-  // waves wait for them after it. One row per thread (BM <= the workgroup's threads, rows in whole waves).
-  constexpr bool DEFER_SCALE = FP8 && NLD > 0 && (NW + NLD) * 64 >= BM && BM % 64 == 0;
+  // The rows' activation scales (float8) and routing weights (plain products) are read only by the
+  // epilogue. With one row per thread in whole waves, their loads (which need the pair loads) go straight
+  // to LDS and stay in flight: loading waves wait for them with their first stages (the K loop's
+  // prologue waits for every load), compute waves of the split roles after the K loop.
+  constexpr bool DEFER = (NW + NLD) * 64 >= BM && BM % 64 == 0;
+  constexpr bool POST_WAIT = DEFER && NLD > 0 && (FP8 || ACT == ACT_NONE);   // compute waves issued some
   for (int r = tid; r < BM; r += (NW + NLD) * 64) {
     const int pair = p.rows[pm * BM + r];
     s_pairs[r] = pair;
+    const bool ok = pair < p.n_pairs;
     if constexpr (FP8) {
       const long long src = p.by_token ? pair / p.topk : pair;
-      if constexpr (DEFER_SCALE)
-        dma4(pair < p.n_pairs ? (const void*)(p.a_scale + src) : (const void*)g_zero16,
-             (FLIDE_LDS_AS char*)s_ascale + (r & ~63) * 4);
-      else s_ascale[r] = pair < p.n_pairs ? p.a_scale[src] : 0.f;
+      if constexpr (DEFER)
+        dma4(ok ? (const void*)(p.a_scale + src) : (const void*)g_zero16, (FLIDE_LDS_AS char*)s_ascale + (r & ~63) * 4);
+      else s_ascale[r] = ok ? p.a_scale[src] : 0.f;
     }
-    if constexpr (ACT == ACT_NONE) s_wt[r] = p.weights && pair < p.n_pairs ? p.weights[pair] : 1.f;
+    if constexpr (ACT == ACT_NONE) {
+      if constexpr (DEFER)
+        dma4(ok && p.weights ? (const void*)(p.weights + pair) : (const void*)&g_one, (FLIDE_LDS_AS char*)s_wt + (r & ~63) * 4);
+      else s_wt[r] = p.weights && ok ? p.weights[pair] : 1.f;
+    }
   }
   lds_barrier();   // the weight loads of the first stages stay in flight
 
@@ -490,7 +496,7 @@ __global__ __launch_bounds__((WAVES_M * WAVES_N + NLD) * 64, OCC) void grouped_d
     kloop(std::integral_constant<int, FM>{}, lds0, lds1, lds2, lds3);
   }
 
-  if constexpr (DEFER_SCALE) {
+  if constexpr (POST_WAIT) {
     wait_vmcnt<0>();
     ring_barrier();   // the scales are in LDS, and every compute wave is done reading the ring
   }
@@ -507,7 +513,7 @@ __global__ __launch_bounds__((WAVES_M * WAVES_N + NLD) * 64, OCC) void grouped_d
       constexpr int TC = BN / 2;
       static_assert(BM * TC * 2 <= STAGE, "the staged tile fits a ring slot");
       S* tile = (S*)lds0;
-      if constexpr (!DEFER_SCALE) ring_barrier();   // every compute wave is done reading the ring
+      if constexpr (!POST_WAIT) ring_barrier();   // every compute wave is done reading the ring
       if (wave_live) {
 #pragma unroll
         for (int fm = 0; fm < FM; ++fm) {
