@@ -21,13 +21,12 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 // ---------------------------------------------------------------------------------------------------
 FLIDE_DEV float bf16_to_f32(u16 v) { return __uint_as_float((uint32_t)v << 16); }
 
-// float32 -> bfloat16 bits, round to nearest even; NaN stays a (quiet) NaN.
-FLIDE_DEV u16 f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (u16)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (u16)(u >> 16);
-}
+// float32 -> bfloat16 bits, round to nearest even; NaN stays a quiet NaN. A __bf16 conversion compiles
+// to gfx950's v_cvt_pk_bf16_f32 (one instruction, two values when the compiler pairs them), which was
+// checked on the GPU against the integer form, (u + 0x7fff + lsb) >> 16 and (u >> 16) | 0x40 for NaN,
+// over all 2^32 inputs: identical, NaN payloads and subnormals included. The integer form with an early
+// return for NaN compiled to exec-mask branches around every conversion of an epilogue.
+FLIDE_DEV u16 f32_to_bf16(float f) { return __builtin_bit_cast(u16, (__bf16)f); }
 
 FLIDE_DEV float f16_to_f32(u16 v) { return (float)__builtin_bit_cast(_Float16, v); }
 FLIDE_DEV u16 f32_to_f16(float f) { return __builtin_bit_cast(u16, (_Float16)f); }
