@@ -618,7 +618,7 @@ __global__ __launch_bounds__((WAVES_M * WAVES_N + NLD) * 64, OCC) void grouped_d
 //
 // Arithmetic: the same 128-wide K steps, lane mapping, MFMA and epilogue order as grouped_dma, so the
 // output bits are the same.
-template <typename OutT, int NS, int BN, int KT_MAX, int XB, int NLD, bool WIDE>
+template <typename OutT, int NS, int BN, int KT_MAX, int XB, int NLD, bool WIDE, bool AREG = false>
 __global__ __launch_bounds__((8 + NLD) * 64, 1) void grouped_fp8_resident(GroupArgs p, int tpb, int nch) {
   constexpr int BM = 128, ROWB = 128;
   // compute waves: WIDE (16-bit outputs, aligned): 8 x 1 waves of 16 rows x BN columns, each wave owning
@@ -629,9 +629,10 @@ __global__ __launch_bounds__((8 + NLD) * 64, 1) void grouped_fp8_resident(GroupA
   constexpr int LBW = LB / NLD;               // weight loads per loader wave and stage
   static_assert(LB % NLD == 0 && (NLD == 1 || LW <= NLD), "loaders split the stage evenly");
   static_assert((NS - 1) * (LBW + LW) < 64 && 2 * KT_MAX < 64, "loads in flight must fit vmcnt");
-  static_assert(NS >= 3 && NS <= 6 && BN % 64 == 0 && FN >= 1, "ring of 3..6 slots, 64-row multiples");
+  static_assert(NS >= 3 && NS <= 7 && BN % 64 == 0 && FN >= 1, "ring of 3..7 slots, 64-row multiples");
+  static_assert(!AREG || (WIDE && FM == 1), "operand rows in registers: one 16-row fragment per wave");
 
-  __shared__ __attribute__((aligned(1024))) char s_a[KT_MAX * A_KT];
+  __shared__ __attribute__((aligned(1024))) char s_a[AREG ? 16 : KT_MAX * A_KT];
   __shared__ __attribute__((aligned(1024))) char s_b[NS * B_BYTES];
   __shared__ __attribute__((aligned(16))) float s_ws[2][BN];
   __shared__ int s_pairs[BM];
@@ -695,7 +696,8 @@ __global__ __launch_bounds__((8 + NLD) * 64, 1) void grouped_fp8_resident(GroupA
       for (int s = 0; s < NS - 1 && s < S; ++s) issue(s);
       for (int s = 0; s < S; ++s) {
         const int ahead = min(NS - 2, S - 1 - s);   // stages after s already in flight
-        if (NS > 5 && ahead >= 4) wait_vmcnt<(NS > 5 ? 4 : 0) * LPS>();
+        if (NS > 6 && ahead >= 5) wait_vmcnt<(NS > 6 ? 5 : 0) * LPS>();
+        else if (NS > 5 && ahead >= 4) wait_vmcnt<(NS > 5 ? 4 : 0) * LPS>();
         else if (NS > 4 && ahead >= 3) wait_vmcnt<(NS > 4 ? 3 : 0) * LPS>();
         else if (NS > 3 && ahead >= 2) wait_vmcnt<(NS > 3 ? 2 : 0) * LPS>();
         else if (ahead >= 1) wait_vmcnt<LPS>();
@@ -712,7 +714,7 @@ __global__ __launch_bounds__((8 + NLD) * 64, 1) void grouped_fp8_resident(GroupA
   }
 
   // ---------------- compute waves ----------------
-  {
+  if constexpr (!AREG) {
     const char* A = (const char*)p.a;
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
@@ -846,7 +848,108 @@ __global__ __launch_bounds__((8 + NLD) * 64, 1) void grouped_fp8_resident(GroupA
       if (++kt == KT) { kt = 0; ++t; }
     }
   };
-  if constexpr (FM == 1) {
+  // AREG (the WIDE layout): lane (r, g) of wave w holds row 16 w + r's K chunks g and g + 4 of every
+  // 128-wide k-tile, the MFMA's A operand for that k-tile, loaded once per block straight from global
+  // memory into registers. The LDS then holds only the weight ring, deep enough (7 slots: six 16 KB
+  // stages in flight per CU instead of two) that the weight stream is no longer bound by the bytes a
+  // CU keeps in flight.
+  auto run_areg = [&](auto fma_tag) {
+    constexpr int FMA = decltype(fma_tag)::value;
+    i32x8_t areg[KT_MAX];
+    if constexpr (FMA > 0) {
+      const int pair = s_pairs[wave * 16 + r];
+      const long long src = pair < p.n_pairs ? (p.by_token ? pair / p.topk : pair) : 0;
+      const char* ar = (const char*)p.a + src * p.sa;
+#pragma unroll
+      for (int kt = 0; kt < KT_MAX; ++kt) {   // chunks past K are zeros
+        const int k0 = kt * ROWB + g * 16, k1 = k0 + 64;
+        uint4 lo = make_uint4(0u, 0u, 0u, 0u), hi = lo;
+        if (k0 < K) lo = *(const uint4*)(ar + k0);
+        if (k1 < K) hi = *(const uint4*)(ar + k1);
+        areg[kt] = i32x8_t{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+      }
+    }
+    f32x4_t acc[FN];
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn) acc[fn] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    int prow[4];
+    float rsc[4], rwt[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {   // output register i: row 16 w + g * 4 + i
+      const int row = wave * 16 + g * 4 + i;
+      prow[i] = s_pairs[row];
+      rsc[i] = s_ascale[row];
+      rwt[i] = s_wt[row];
+    }
+    const bool mulw = p.weights != nullptr;
+    int slot = 0;
+    for (int t = t0; t < t0 + nt; ++t) {
+#pragma unroll
+      for (int kt = 0; kt < KT_MAX; ++kt) {
+        if (kt < KT) {
+          ring_barrier();
+          asm volatile("" ::: "memory");
+          if constexpr (FMA > 0) {
+            const char* sb_ = s_b + slot * B_BYTES;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {   // the tile's columns in two halves (registers)
+              i32x8_t bfr[FN / 2];
+#pragma unroll
+              for (int fn = 0; fn < FN / 2; ++fn) {
+                const char* fb = sb_ + (h * (FN / 2) + fn) * 16 * ROWB;
+                const u32x4_t lo = *(const u32x4_t*)(fb + lane_off[0]);
+                const u32x4_t hi = *(const u32x4_t*)(fb + lane_off[1]);
+                bfr[fn] = i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+              }
+#pragma unroll
+              for (int fn = 0; fn < FN / 2; ++fn)
+                acc[h * (FN / 2) + fn] = mfma_fp8(areg[kt], bfr[fn], acc[h * (FN / 2) + fn]);
+            }
+          }
+          if (++slot == NS) slot = 0;
+        }
+      }
+      if constexpr (FMA > 0) {   // epilogue of tile t, 4 rows at a time through LDS, as the WIDE layout above
+        float cs[FN];
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn) cs[fn] = s_ws[t & 1][fn * 16 + r];
+        uint16_t* stg = s_stage[wave];
+        const int c8 = (l & 15) * 8;
+        const int col0 = t * BN + c8;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+          for (int fn = 0; fn < FN; ++fn) {
+            float v = acc[fn][i] * rsc[i] * cs[fn];
+            if (mulw) v *= rwt[i];
+            stg[g * BN + fn * 16 + r] = OutTraits<OutT>::conv(v);
+          }
+          __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): the wave's staging writes are done
+          const uint4 q = *(const uint4*)(stg + g * BN + c8);
+          const int pair = prow[i];
+          if (pair < p.n_pairs && col0 < p.N) {
+            uint16_t* o = (uint16_t*)p.out + (long long)pair * p.sc + col0;
+            if (col0 + 8 <= p.N) {
+              *(uint4*)o = q;
+            } else {
+              const uint16_t e[8] = {(uint16_t)(q.x & 0xffff), (uint16_t)(q.x >> 16), (uint16_t)(q.y & 0xffff),
+                                     (uint16_t)(q.y >> 16), (uint16_t)(q.z & 0xffff), (uint16_t)(q.z >> 16),
+                                     (uint16_t)(q.w & 0xffff), (uint16_t)(q.w >> 16)};
+#pragma unroll
+              for (int j = 0; j < 7; ++j)
+                if (col0 + j < p.N) o[j] = e[j];
+            }
+          }
+        }
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn) acc[fn] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      }
+    }
+  };
+  if constexpr (AREG) {
+    if (nlive == 0) run_areg(std::integral_constant<int, 0>{});
+    else run_areg(std::integral_constant<int, 1>{});
+  } else if constexpr (FM == 1) {
     if (nlive == 0) run(std::integral_constant<int, 0>{});
     else run(std::integral_constant<int, 1>{});
   } else {
@@ -881,6 +984,12 @@ int launch_fp8_resident(GroupArgs& p, hipStream_t st) {
   typedef typename OutTraits<OutT>::storage S;
   if constexpr (sizeof(S) == 2) {
     if (p.sc % 8 == 0 && (uintptr_t)p.out % 16 == 0) {
+      // K of 641..768 (six k-tiles, as the 704-wide down product) with 16-byte aligned activation rows:
+      // the rows in registers and a 7-slot weight ring (its column scales need KT >= 6 slots of lead)
+      if ((p.K + 127) / 128 == KT_MAX && p.sa % 16 == 0 && (uintptr_t)p.a % 16 == 0) {
+        grouped_fp8_resident<OutT, 7, BN, KT_MAX, XB, NLD, true, true><<<grid, block, 0, st>>>(p, tpb, nch);
+        return FLIDE_MOE_OK;
+      }
       grouped_fp8_resident<OutT, NS, BN, KT_MAX, XB, NLD, true><<<grid, block, 0, st>>>(p, tpb, nch);
       return FLIDE_MOE_OK;
     }
