@@ -1021,6 +1021,350 @@ int launch_fp8_resident(GroupArgs& p, hipStream_t st) {
 //     whole 128-byte lines per row and stage read measurably faster than the half-line pairs of the
 //     register-streaming kernel (gate/up 180 -> 170 us, down 112 -> 94 us at 64 tokens; fp8 110 ->
 //     95 / 61 -> 52 us)
+// ---------------------------------------------------------------------------------------------------
+// Persistent float8 gated product: bm 128, BN 256, split roles, staged epilogue
+// ---------------------------------------------------------------------------------------------------
+// At 4096 tokens the per-tile kernel spends about a third of a float8 gate/up tile's life outside its K
+// loop: the start-up chain (the item's expert, its pairs, the first stages) and the epilogue, while the
+// CU's load pipe idles. Here one workgroup per CU walks the items of its XCD's range (items j, j + W,
+// j + 2W, ... of the range for the W workgroups of that XCD, the order in which the per-tile launch's
+// workgroups are dispatched) and the stage ring runs on across items. During an item's K loop, compute
+// wave 0 finds the next item's block, column tile and expert, waves 0-1 bring its pairs and activation
+// scales into the other half of double-buffered LDS, and every compute wave loads its column scales; the
+// loader waves build the next item's operand offsets and switch to them two stages before the item
+// ends, so its first stages land during this item's last MFMAs and epilogue. The next item's metadata
+// moves only through LDS, written after one stage barrier and read after a later one (see act()).
+// Barriers per item, for every wave: the item's nk stage barriers, then two in the epilogue.
+// The arithmetic is grouped_dma's float8 gated path (K steps, MFMA order, epilogue), so the bits are too.
+template <typename OutT, int ACT>
+__global__ __launch_bounds__(12 * 64, 1) void grouped_fp8_gated_persist(GroupArgs p) {
+  constexpr int BM = 128, BN = 256, NS = 3, ROWB = 128, NW = 8, NLD = 4, WAVES_M = 2;
+  constexpr int CPR = 8, RPI = 8, KS = 128;   // float8: 128 K per 128-byte stage row
+  constexpr int A_BYTES = BM * ROWB, STAGE = A_BYTES + BN * ROWB;
+  constexpr int LA = BM / (NLD * RPI), LB = BN / (NLD * RPI), L = LA + LB;
+  constexpr int WM = BM / WAVES_M, WN = BN / (NW / WAVES_M), FM = WM / 16, FN = WN / 16, TC = BN / 2;
+  static_assert(FM == 4 && FN == 4 && (NS - 1) * L < 64, "2 x 4 waves of 64 x 64, loads in flight fit vmcnt");
+  typedef typename OutTraits<OutT>::storage S;
+  typedef typename OutRound<OutT>::type RT;   // the gate/up values' rounding
+  static_assert(sizeof(S) == 2, "16-bit outputs");
+  __shared__ __attribute__((aligned(1024))) char lds0[STAGE];
+  __shared__ __attribute__((aligned(1024))) char lds1[STAGE];
+  __shared__ __attribute__((aligned(1024))) char lds2[STAGE];
+  __shared__ int s_pairs[2][BM];
+  __shared__ float s_ascale[2][BM];
+  __shared__ int s_meta[2][4];   // the item's block, column tile and expert
+
+  const int tid = threadIdx.x, l = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int K = p.K, half = p.N / 2, nk = K / KS;
+  // this workgroup's items: XCD x's range of the items in use, every W-th from j
+  const int nused = *p.used / BM;
+  const long long R = (long long)nused * p.ntn;
+  const int x = blockIdx.x & 7, W = gridDim.x >> 3, j = blockIdx.x >> 3;
+  const long long it0 = R * x / 8 + j, it_end = R * (x + 1) / 8;
+  const int n_items = it0 < it_end ? (int)((it_end - it0 + W - 1) / W) : 0;
+  if (n_items == 0) return;
+
+  // item -> (block, column tile, expert) in grouped_dma's prefill order (column-tile major inside an
+  // expert), by one wave: expert_run's window loads, issued apart from their use
+  int wlo = 0, whi = 0;
+  auto window = [&](long long it) {
+    const int blk = (int)(it / p.ntn);
+    const int li = blk - 63 + l, hi = blk + l;
+    wlo = li >= 0 ? p.blocks[li] : -1;
+    whi = hi < nused ? p.blocks[hi] : -1;
+  };
+  auto resolve = [&](long long it, int* meta) {
+    const int blk = (int)(it / p.ntn);
+    const int e = __builtin_amdgcn_readfirstlane(whi);   // lane 0 read blocks[blk]
+    const unsigned long long ml = __ballot(wlo != e), mh = __ballot(whi != e);
+    const int s0 = __builtin_amdgcn_readfirstlane(
+        ml ? blk - 63 + (63 - __builtin_clzll(ml)) + 1 : expert_first_block(p.blocks, blk - 64, e, l));
+    const int s1 = __builtin_amdgcn_readfirstlane(
+        mh ? blk + __builtin_ctzll(mh) : expert_end_block(p.blocks, blk + 64, e, nused, l));
+    const int local = (int)(it - (long long)s0 * p.ntn), nb = s1 - s0;
+    if (l == 0) {
+      meta[0] = s0 + local % nb;
+      meta[1] = local / nb;
+      meta[2] = e;
+    }
+  };
+  auto scale_of = [&](int pair) {
+    return pair < p.n_pairs ? p.a_scale[p.by_token ? pair / p.topk : pair] : 0.f;
+  };
+
+  // start-up: the first item's metadata, pairs and scales
+  if (wave == 0) {
+    window(it0);
+    resolve(it0, s_meta[0]);
+  }
+  lds_barrier();
+  if (tid < BM) {
+    const int pair = p.rows[s_meta[0][0] * BM + tid];
+    s_pairs[0][tid] = pair;
+    s_ascale[0][tid] = scale_of(pair);
+  }
+  lds_barrier();
+
+  if (wave >= NW) {   // ---------------- loaders ----------------
+    const int lw = wave - NW;
+    const int kc = ((l % CPR) ^ swz<CPR>(l / CPR)) * 16;   // this lane's chunk's K offset (bytes)
+    const long long a_rows = p.by_token ? (p.n_pairs + p.topk - 1) / p.topk : p.n_pairs;
+    const __amdgpu_buffer_rsrc_t rsA = buf_rsrc(p.a, (a_rows - 1) * p.sa + K);
+    __amdgpu_buffer_rsrc_t rsB[2];
+    uint32_t b_off[2][LB], a_off[2][LA];   // [item parity]
+    auto set_ops = [&](int buf) {   // the operands of the item whose metadata is in buffer buf
+      const int pn = __builtin_amdgcn_readfirstlane(s_meta[buf][1]);
+      const long long e = __builtin_amdgcn_readfirstlane(s_meta[buf][2]);
+      rsB[buf] = buf_rsrc((const char*)p.w + e * p.sbe, (long long)(p.N - 1) * p.sbn + K);
+#pragma unroll
+      for (int i = 0; i < LB; ++i) {
+        const int row = (lw * LB + i) * RPI + l / CPR;
+        int cc = pn * TC + (row < TC ? row : row - TC);
+        if (cc >= half) cc = half - 1;
+        const long long n = row < TC ? cc : cc + half;
+        b_off[buf][i] = (uint32_t)(n * p.sbn + kc);
+      }
+#pragma unroll
+      for (int i = 0; i < LA; ++i) {
+        const int pair = s_pairs[buf][(lw * LA + i) * RPI + l / CPR];
+        const long long src = pair < p.n_pairs ? (p.by_token ? pair / p.topk : pair) : 0;
+        a_off[buf][i] = (uint32_t)(src * p.sa + kc);
+      }
+    };
+    auto issue = [&](int slot, int kt, int buf) {   // stage kt of the item in buffer buf, into ring slot
+      FLIDE_LDS_AS char* sb = (FLIDE_LDS_AS char*)(slot == 0 ? lds0 : slot == 1 ? lds1 : lds2);
+      const uint32_t kb = (uint32_t)(kt * KS);
+#pragma unroll
+      for (int i = 0; i < LA; ++i) dma16b<0>(rsA, a_off[buf][i], kb, sb + (lw * LA + i) * 1024);
+#pragma unroll
+      for (int i = 0; i < LB; ++i) dma16b<0>(rsB[buf], b_off[buf][i], kb, sb + A_BYTES + (lw * LB + i) * 1024);
+    };
+    set_ops(0);
+#pragma unroll
+    for (int st = 0; st < NS - 1; ++st) issue(st, st, 0);
+    const int S_all = n_items * nk;
+    int g = 0;   // global stage
+    for (int n = 0; n < n_items; ++n) {
+      const int buf = n & 1;
+      const bool has_next = n + 1 < n_items;
+      for (int kt = 0; kt < nk; ++kt, ++g) {
+        wait_stage<NS, L>(min(NS - 2, S_all - 1 - g));
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if (kt == 6 && has_next) set_ops(buf ^ 1);   // the compute waves placed its pairs at stage 5
+        const int ks = kt + NS - 1;
+        if (ks < nk) issue((g + NS - 1) % NS, ks, buf);
+        else if (has_next) issue((g + NS - 1) % NS, ks - nk, buf ^ 1);
+      }
+      __builtin_amdgcn_s_barrier();   // the epilogue's two barriers
+      __builtin_amdgcn_s_barrier();
+    }
+    return;
+  }
+
+  // ---------------- compute waves ----------------
+  const int wm = wave % WAVES_M, wn = wave / WAVES_M;
+  const int r = l & 15, g = l >> 4;
+  int lane_off[2];
+#pragma unroll
+  for (int jj = 0; jj < 2; ++jj) lane_off[jj] = r * ROWB + ((((jj * 4 + g) % CPR) ^ swz<CPR>(r)) << 4);
+  auto a_off = [&](int fm, int jj) { return (wm * WM + fm * 16) * ROWB + lane_off[jj]; };
+  auto b_off = [&](int fn, int jj) {   // gate fragments first, then the matching up fragments
+    const int f = fn < FN / 2 ? fn : fn - FN / 2;
+    return A_BYTES + ((fn < FN / 2 ? 0 : TC) + wn * (WN / 2) + f * 16) * ROWB + lane_off[jj];
+  };
+  f32x4_t acc[FM][FN];
+  int g_stage = 0;
+  int pair_next = 0;
+  float scale_next = 0.f;
+  for (int n = 0; n < n_items; ++n) {
+    const int buf = n & 1, nbuf = buf ^ 1;
+    const bool has_next = n + 1 < n_items;
+    const long long it_next = it0 + (long long)(n + 1) * W;
+    // the next item's metadata, after this item's stage barrier k (nk >= 10)
+    auto act = [&](int k) {
+      if (!has_next) return;
+      if (k == 0 && wave == 0) window(it_next);
+      if (k == 2 && wave == 0) resolve(it_next, s_meta[nbuf]);
+      if (k == 3 && tid < BM) pair_next = p.rows[s_meta[nbuf][0] * BM + tid];   // s_meta written before barrier 3
+      if (k == 5 && tid < BM) {   // the loaders read the pairs after barrier 6
+        s_pairs[nbuf][tid] = pair_next;
+        scale_next = scale_of(pair_next);
+      }
+      if (k == 8 && tid < BM) s_ascale[nbuf][tid] = scale_next;   // read by that item's epilogue
+    };
+    const int pn = __builtin_amdgcn_readfirstlane(s_meta[buf][1]);
+    // this lane's columns' gate and up scales, read by the epilogue
+    float cs_g[FN / 2], cs_u[FN / 2];
+    {
+      const long long e = __builtin_amdgcn_readfirstlane(s_meta[buf][2]);
+#pragma unroll
+      for (int f = 0; f < FN / 2; ++f) {
+        const int col = pn * TC + wn * (WN / 2) + f * 16 + r;
+        const bool ok = col < half;
+        cs_g[f] = ok ? p.w_scale[e * p.sse + col] : 0.f;
+        cs_u[f] = ok ? p.w_scale[e * p.sse + col + half] : 0.f;
+      }
+    }
+    bool m_live[FM];
+    int nlive = 0;
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm) {
+      m_live[fm] = __builtin_amdgcn_readfirstlane(s_pairs[buf][wm * WM + fm * 16]) < p.n_pairs;
+      nlive += m_live[fm] ? 1 : 0;
+    }
+    const int colbase0 = pn * TC + wn * (WN / 2);
+    const bool wave_live = colbase0 < half && m_live[0];
+    if (colbase0 >= half) nlive = 0;
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn) acc[fm][fn] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    // the item's K loop, barrier in mid-stage as in grouped_dma's split roles
+    auto kloop = [&](auto fma_tag, char* __restrict__ s0, char* __restrict__ s1, char* __restrict__ s2) {
+      constexpr int FMA = decltype(fma_tag)::value;
+      auto slot_ptr = [&](int slot) -> char* { return slot == 0 ? s0 : slot == 1 ? s1 : s2; };
+      if constexpr (FMA == 0) {
+        for (int k = 0; k < nk; ++k) {
+          ring_barrier();
+          asm volatile("" ::: "memory");
+          act(k);
+        }
+      } else {
+        constexpr int H1 = FMA < 2 ? FMA : 2;
+        u32x4_t af[FMA][2], bfr[FN][2];
+        auto read_a = [&](const char* sb, int fm) {
+          af[fm][0] = *(const u32x4_t*)(sb + a_off(fm, 0));
+          af[fm][1] = *(const u32x4_t*)(sb + a_off(fm, 1));
+        };
+        auto read_rest = [&](const char* sb) {
+#pragma unroll
+          for (int fn = 0; fn < FN; ++fn) {
+            bfr[fn][0] = *(const u32x4_t*)(sb + b_off(fn, 0));
+            bfr[fn][1] = *(const u32x4_t*)(sb + b_off(fn, 1));
+          }
+#pragma unroll
+          for (int fm = H1; fm < FMA; ++fm) read_a(sb, fm);
+        };
+        auto rows = [&](auto lo_tag, auto hi_tag) {
+#pragma unroll
+          for (int fm = decltype(lo_tag)::value; fm < decltype(hi_tag)::value; ++fm)
+#pragma unroll
+            for (int fn = 0; fn < FN; ++fn) {
+              const u32x4_t *a = af[fm], *b = bfr[fn];
+              acc[fm][fn] = mfma_fp8(i32x8_t{(int)a[0][0], (int)a[0][1], (int)a[0][2], (int)a[0][3], (int)a[1][0], (int)a[1][1], (int)a[1][2], (int)a[1][3]},
+                                     i32x8_t{(int)b[0][0], (int)b[0][1], (int)b[0][2], (int)b[0][3], (int)b[1][0], (int)b[1][1], (int)b[1][2], (int)b[1][3]},
+                                     acc[fm][fn]);
+            }
+        };
+        int slot = g_stage % NS;
+        ring_barrier();
+        asm volatile("" ::: "memory");
+        act(0);
+#pragma unroll
+        for (int fm = 0; fm < H1; ++fm) read_a(slot_ptr(slot), fm);
+        read_rest(slot_ptr(slot));
+        for (int kt = 0; kt + 1 < nk; ++kt) {
+          const int nxt = slot + 1 == NS ? 0 : slot + 1;
+          rows(std::integral_constant<int, 0>{}, std::integral_constant<int, H1>{});
+          __builtin_amdgcn_sched_barrier(0);   // those MFMAs issue before the barrier
+          ring_barrier();
+          asm volatile("" ::: "memory");
+          act(kt + 1);
+          const char* sb = slot_ptr(nxt);
+#pragma unroll
+          for (int fm = 0; fm < H1; ++fm) read_a(sb, fm);
+          rows(std::integral_constant<int, H1>{}, std::integral_constant<int, FMA>{});
+          read_rest(sb);
+          slot = nxt;
+        }
+        rows(std::integral_constant<int, 0>{}, std::integral_constant<int, FMA>{});
+      }
+    };
+    if (nlive == 0) kloop(std::integral_constant<int, 0>{}, lds0, lds1, lds2);
+    else if (nlive == 1) kloop(std::integral_constant<int, 1>{}, lds0, lds1, lds2);
+    else if (nlive == 2) kloop(std::integral_constant<int, 2>{}, lds0, lds1, lds2);
+    else if (nlive == 3) kloop(std::integral_constant<int, 3>{}, lds0, lds1, lds2);
+    else kloop(std::integral_constant<int, 4>{}, lds0, lds1, lds2);
+    const int last = (g_stage + nk - 1) % NS;   // the ring slot of the item's last stage
+    g_stage += nk;
+
+    // epilogue: the BM x TC activation tile staged in the last stage's slot (the loaders refill it only
+    // after the next item's first barrier), then 16-byte row pieces
+    wait_vmcnt<0>();   // the column scales, the next item's pair and scale loads
+    ring_barrier();    // every compute wave is done reading the ring
+    S* tile = (S*)(last == 0 ? lds0 : last == 1 ? lds1 : lds2);
+    if (wave_live) {
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm) {
+        if (!m_live[fm]) continue;
+        const int row0 = wm * WM + fm * 16;
+        float rs[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) rs[i] = s_ascale[buf][row0 + g * 4 + i];
+#pragma unroll
+        for (int f = 0; f < FN / 2; ++f) {
+          const int lc = wn * (WN / 2) + f * 16 + r;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {   // the values store_frag computes, in the same order
+            const float gg = round_in<RT>(acc[fm][f][i] * rs[i] * cs_g[f]);
+            const float uu = round_in<RT>(acc[fm][f + FN / 2][i] * rs[i] * cs_u[f]);
+            tile[(row0 + g * 4 + i) * TC + lc] = OutTraits<OutT>::conv(act_f32<ACT>(gg, uu));
+          }
+        }
+      }
+    }
+    ring_barrier();
+    constexpr int LPR = TC / 8;          // lanes per row, 8 columns each
+    constexpr int RPP = NW * 64 / LPR;   // rows per pass
+    const int c8 = (tid % LPR) * 8;
+    const int col0 = pn * TC + c8;
+    for (int rr = tid / LPR; rr < BM; rr += RPP) {
+      const int pair = s_pairs[buf][rr];
+      if (pair >= p.n_pairs || col0 >= half) continue;
+      const uint4 q = *(const uint4*)(tile + rr * TC + c8);
+      S* o = (S*)p.out + (long long)pair * p.sc + col0;
+      if (col0 + 8 <= half) {
+        *(uint4*)o = q;
+      } else {
+        const S ev[8] = {(S)(q.x & 0xffff), (S)(q.x >> 16), (S)(q.y & 0xffff), (S)(q.y >> 16),
+                         (S)(q.z & 0xffff), (S)(q.z >> 16), (S)(q.w & 0xffff), (S)(q.w >> 16)};
+#pragma unroll
+        for (int jj = 0; jj < 7; ++jj)
+          if (col0 + jj < half) o[jj] = ev[jj];
+      }
+    }
+  }
+}
+
+// the persistent float8 gated product where it applies: 16-bit outputs in 16-byte aligned rows, no
+// routing weights, K a multiple of 128 with at least 10 stages (the next item's metadata needs stages
+// 0-8 of the current one); one workgroup per CU, a multiple of 8
+template <typename OutT, int ACT>
+int launch_fp8_gated_persist(GroupArgs& p, hipStream_t st) {
+  typedef typename OutTraits<OutT>::storage S;
+  if constexpr (sizeof(S) != 2) {
+    return FLIDE_MOE_ERR_TILE;
+  } else {
+    if (p.weights || p.sc % 8 || (uintptr_t)p.out % 16 || p.K % 128 || p.K / 128 < 10) return FLIDE_MOE_ERR_TILE;
+    static int cus[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return FLIDE_MOE_ERR_TILE;
+    if (cus[dev] == 0) {
+      int n = 0;
+      if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 8)
+        return FLIDE_MOE_ERR_TILE;
+      cus[dev] = n / 8 * 8;
+    }
+    p.ntn = (p.N / 2 + 127) / 128;
+    p.pack_f32 = 0;
+    grouped_fp8_gated_persist<OutT, ACT><<<dim3(cus[dev]), dim3(12 * 64), 0, st>>>(p);
+    return FLIDE_MOE_OK;
+  }
+}
+
 constexpr int DMA_BN = 256;
 
 template <typename T, typename OutT, int ACT, int BM, int WM_, int WN_, int NS, int ROWB, int OCC, int XB,
@@ -1068,7 +1412,10 @@ int launch_dma(GroupArgs& p, int bm, hipStream_t st) {
         if (launch_fp8_resident<OutT>(p, st) == FLIDE_MOE_OK) return FLIDE_MOE_OK;
         return launch_one<T, OutT, ACT, 128, 2, 4, 2, 128, 2, 4, 128>(p, st);
       }
-      else return launch_one<T, OutT, ACT, 128, 2, 4, 3, 128, 1, 4, 256, 4>(p, st);   // + 4 loader waves
+      else {
+        if (launch_fp8_gated_persist<OutT, ACT>(p, st) == FLIDE_MOE_OK) return FLIDE_MOE_OK;
+        return launch_one<T, OutT, ACT, 128, 2, 4, 3, 128, 1, 4, 256, 4>(p, st);   // + 4 loader waves
+      }
     }
     if (bm == 64) return launch_one<T, OutT, ACT, 64, 1, 4, 2, 128, 2, 8, 128>(p, st);
   } else {
