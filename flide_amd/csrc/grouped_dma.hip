@@ -1022,7 +1022,7 @@ int launch_fp8_resident(GroupArgs& p, hipStream_t st) {
 //     register-streaming kernel (gate/up 180 -> 170 us, down 112 -> 94 us at 64 tokens; fp8 110 ->
 //     95 / 61 -> 52 us)
 // ---------------------------------------------------------------------------------------------------
-// Persistent float8 gated product: bm 128, BN 256, split roles, staged epilogue
+// Persistent gated product (float8 or 16-bit): bm 128, BN 256, split roles, staged epilogue
 // ---------------------------------------------------------------------------------------------------
 // At 4096 tokens the per-tile kernel spends about a third of a float8 gate/up tile's life outside its K
 // loop: the start-up chain (the item's expert, its pairs, the first stages) and the epilogue, while the
@@ -1035,17 +1035,20 @@ int launch_fp8_resident(GroupArgs& p, hipStream_t st) {
 // ends, so its first stages land during this item's last MFMAs and epilogue. The next item's metadata
 // moves only through LDS, written after one stage barrier and read after a later one (see act()).
 // Barriers per item, for every wave: the item's nk stage barriers, then two in the epilogue.
-// The arithmetic is grouped_dma's float8 gated path (K steps, MFMA order, epilogue), so the bits are too.
-template <typename OutT, int ACT>
-__global__ __launch_bounds__(12 * 64, 1) void grouped_fp8_gated_persist(GroupArgs p) {
+// The arithmetic is grouped_dma's gated path (K steps, MFMA order, epilogue), so the bits are too.
+// 16-bit weights: 64 K per 128-byte stage row as two 32-wide MFMA steps, no scales.
+template <typename T, typename OutT, int ACT>
+__global__ __launch_bounds__(12 * 64, 1) void grouped_gated_persist(GroupArgs p) {
+  constexpr bool FP8 = std::is_same<T, Fp8Tag>::value;
+  constexpr int EB = DmaElem<T>::BYTES;
   constexpr int BM = 128, BN = 256, NS = 3, ROWB = 128, NW = 8, NLD = 4, WAVES_M = 2;
-  constexpr int CPR = 8, RPI = 8, KS = 128;   // float8: 128 K per 128-byte stage row
+  constexpr int CPR = 8, RPI = 8, KS = ROWB / EB;   // K per 128-byte stage row
   constexpr int A_BYTES = BM * ROWB, STAGE = A_BYTES + BN * ROWB;
   constexpr int LA = BM / (NLD * RPI), LB = BN / (NLD * RPI), L = LA + LB;
   constexpr int WM = BM / WAVES_M, WN = BN / (NW / WAVES_M), FM = WM / 16, FN = WN / 16, TC = BN / 2;
   static_assert(FM == 4 && FN == 4 && (NS - 1) * L < 64, "2 x 4 waves of 64 x 64, loads in flight fit vmcnt");
   typedef typename OutTraits<OutT>::storage S;
-  typedef typename OutRound<OutT>::type RT;   // the gate/up values' rounding
+  typedef typename std::conditional<FP8, typename OutRound<OutT>::type, T>::type RT;   // gate/up rounding
   static_assert(sizeof(S) == 2, "16-bit outputs");
   __shared__ __attribute__((aligned(1024))) char lds0[STAGE];
   __shared__ __attribute__((aligned(1024))) char lds1[STAGE];
@@ -1090,6 +1093,7 @@ __global__ __launch_bounds__(12 * 64, 1) void grouped_fp8_gated_persist(GroupArg
     }
   };
   auto scale_of = [&](int pair) {
+    if constexpr (!FP8) return 1.f;
     return pair < p.n_pairs ? p.a_scale[p.by_token ? pair / p.topk : pair] : 0.f;
   };
 
@@ -1110,31 +1114,31 @@ __global__ __launch_bounds__(12 * 64, 1) void grouped_fp8_gated_persist(GroupArg
     const int lw = wave - NW;
     const int kc = ((l % CPR) ^ swz<CPR>(l / CPR)) * 16;   // this lane's chunk's K offset (bytes)
     const long long a_rows = p.by_token ? (p.n_pairs + p.topk - 1) / p.topk : p.n_pairs;
-    const __amdgpu_buffer_rsrc_t rsA = buf_rsrc(p.a, (a_rows - 1) * p.sa + K);
+    const __amdgpu_buffer_rsrc_t rsA = buf_rsrc(p.a, ((a_rows - 1) * p.sa + K) * EB);
     __amdgpu_buffer_rsrc_t rsB[2];
     uint32_t b_off[2][LB], a_off[2][LA];   // [item parity]
     auto set_ops = [&](int buf) {   // the operands of the item whose metadata is in buffer buf
       const int pn = __builtin_amdgcn_readfirstlane(s_meta[buf][1]);
       const long long e = __builtin_amdgcn_readfirstlane(s_meta[buf][2]);
-      rsB[buf] = buf_rsrc((const char*)p.w + e * p.sbe, (long long)(p.N - 1) * p.sbn + K);
+      rsB[buf] = buf_rsrc((const char*)p.w + e * p.sbe * EB, ((long long)(p.N - 1) * p.sbn + K) * EB);
 #pragma unroll
       for (int i = 0; i < LB; ++i) {
         const int row = (lw * LB + i) * RPI + l / CPR;
         int cc = pn * TC + (row < TC ? row : row - TC);
         if (cc >= half) cc = half - 1;
         const long long n = row < TC ? cc : cc + half;
-        b_off[buf][i] = (uint32_t)(n * p.sbn + kc);
+        b_off[buf][i] = (uint32_t)(n * p.sbn * EB + kc);
       }
 #pragma unroll
       for (int i = 0; i < LA; ++i) {
         const int pair = s_pairs[buf][(lw * LA + i) * RPI + l / CPR];
         const long long src = pair < p.n_pairs ? (p.by_token ? pair / p.topk : pair) : 0;
-        a_off[buf][i] = (uint32_t)(src * p.sa + kc);
+        a_off[buf][i] = (uint32_t)(src * p.sa * EB + kc);
       }
     };
     auto issue = [&](int slot, int kt, int buf) {   // stage kt of the item in buffer buf, into ring slot
       FLIDE_LDS_AS char* sb = (FLIDE_LDS_AS char*)(slot == 0 ? lds0 : slot == 1 ? lds1 : lds2);
-      const uint32_t kb = (uint32_t)(kt * KS);
+      const uint32_t kb = (uint32_t)(kt * ROWB);
 #pragma unroll
       for (int i = 0; i < LA; ++i) dma16b<0>(rsA, a_off[buf][i], kb, sb + (lw * LA + i) * 1024);
 #pragma unroll
@@ -1203,8 +1207,8 @@ __global__ __launch_bounds__(12 * 64, 1) void grouped_fp8_gated_persist(GroupArg
       for (int f = 0; f < FN / 2; ++f) {
         const int col = pn * TC + wn * (WN / 2) + f * 16 + r;
         const bool ok = col < half;
-        cs_g[f] = ok ? p.w_scale[e * p.sse + col] : 0.f;
-        cs_u[f] = ok ? p.w_scale[e * p.sse + col + half] : 0.f;
+        cs_g[f] = !FP8 ? 1.f : ok ? p.w_scale[e * p.sse + col] : 0.f;
+        cs_u[f] = !FP8 ? 1.f : ok ? p.w_scale[e * p.sse + col + half] : 0.f;
       }
     }
     bool m_live[FM];
@@ -1254,9 +1258,14 @@ __global__ __launch_bounds__(12 * 64, 1) void grouped_fp8_gated_persist(GroupArg
 #pragma unroll
             for (int fn = 0; fn < FN; ++fn) {
               const u32x4_t *a = af[fm], *b = bfr[fn];
-              acc[fm][fn] = mfma_fp8(i32x8_t{(int)a[0][0], (int)a[0][1], (int)a[0][2], (int)a[0][3], (int)a[1][0], (int)a[1][1], (int)a[1][2], (int)a[1][3]},
-                                     i32x8_t{(int)b[0][0], (int)b[0][1], (int)b[0][2], (int)b[0][3], (int)b[1][0], (int)b[1][1], (int)b[1][2], (int)b[1][3]},
-                                     acc[fm][fn]);
+              if constexpr (FP8) {
+                acc[fm][fn] = mfma_fp8(i32x8_t{(int)a[0][0], (int)a[0][1], (int)a[0][2], (int)a[0][3], (int)a[1][0], (int)a[1][1], (int)a[1][2], (int)a[1][3]},
+                                       i32x8_t{(int)b[0][0], (int)b[0][1], (int)b[0][2], (int)b[0][3], (int)b[1][0], (int)b[1][1], (int)b[1][2], (int)b[1][3]},
+                                       acc[fm][fn]);
+              } else {   // two 32-wide K steps, in order
+                acc[fm][fn] = Mfma16<T>::mma(a[0], b[0], acc[fm][fn]);
+                acc[fm][fn] = Mfma16<T>::mma(a[1], b[1], acc[fm][fn]);
+              }
             }
         };
         int slot = g_stage % NS;
@@ -1303,7 +1312,7 @@ __global__ __launch_bounds__(12 * 64, 1) void grouped_fp8_gated_persist(GroupArg
         const int row0 = wm * WM + fm * 16;
         float rs[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) rs[i] = s_ascale[buf][row0 + g * 4 + i];
+        for (int i = 0; i < 4; ++i) rs[i] = FP8 ? s_ascale[buf][row0 + g * 4 + i] : 1.f;
 #pragma unroll
         for (int f = 0; f < FN / 2; ++f) {
           const int lc = wn * (WN / 2) + f * 16 + r;
@@ -1339,16 +1348,17 @@ __global__ __launch_bounds__(12 * 64, 1) void grouped_fp8_gated_persist(GroupArg
   }
 }
 
-// the persistent float8 gated product where it applies: 16-bit outputs in 16-byte aligned rows, no
-// routing weights, K a multiple of 128 with at least 10 stages (the next item's metadata needs stages
-// 0-8 of the current one); one workgroup per CU, a multiple of 8
-template <typename OutT, int ACT>
-int launch_fp8_gated_persist(GroupArgs& p, hipStream_t st) {
+// the persistent gated product where it applies: 16-bit outputs in 16-byte aligned rows, no routing
+// weights, K a whole number of stages, at least 10 (the next item's metadata needs stages 0-8 of the
+// current one); one workgroup per CU, a multiple of 8
+template <typename T, typename OutT, int ACT>
+int launch_gated_persist(GroupArgs& p, hipStream_t st) {
+  constexpr int KS = 128 / DmaElem<T>::BYTES;
   typedef typename OutTraits<OutT>::storage S;
   if constexpr (sizeof(S) != 2) {
     return FLIDE_MOE_ERR_TILE;
   } else {
-    if (p.weights || p.sc % 8 || (uintptr_t)p.out % 16 || p.K % 128 || p.K / 128 < 10) return FLIDE_MOE_ERR_TILE;
+    if (p.weights || p.sc % 8 || (uintptr_t)p.out % 16 || p.K % KS || p.K / KS < 10) return FLIDE_MOE_ERR_TILE;
     static int cus[64] = {0};
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return FLIDE_MOE_ERR_TILE;
@@ -1360,7 +1370,7 @@ int launch_fp8_gated_persist(GroupArgs& p, hipStream_t st) {
     }
     p.ntn = (p.N / 2 + 127) / 128;
     p.pack_f32 = 0;
-    grouped_fp8_gated_persist<OutT, ACT><<<dim3(cus[dev]), dim3(12 * 64), 0, st>>>(p);
+    grouped_gated_persist<T, OutT, ACT><<<dim3(cus[dev]), dim3(12 * 64), 0, st>>>(p);
     return FLIDE_MOE_OK;
   }
 }
@@ -1413,7 +1423,7 @@ int launch_dma(GroupArgs& p, int bm, hipStream_t st) {
         return launch_one<T, OutT, ACT, 128, 2, 4, 2, 128, 2, 4, 128>(p, st);
       }
       else {
-        if (launch_fp8_gated_persist<OutT, ACT>(p, st) == FLIDE_MOE_OK) return FLIDE_MOE_OK;
+        if (launch_gated_persist<T, OutT, ACT>(p, st) == FLIDE_MOE_OK) return FLIDE_MOE_OK;
         return launch_one<T, OutT, ACT, 128, 2, 4, 3, 128, 1, 4, 256, 4>(p, st);   // + 4 loader waves
       }
     }
@@ -1426,7 +1436,10 @@ int launch_dma(GroupArgs& p, int bm, hipStream_t st) {
     if (bm == 256) return launch_one<T, OutT, ACT, 256, 1, 4, 4, 64, 1, 2>(p, st);
     if (bm == 128) {   // 8 waves of 64 x 64, two per SIMD within one workgroup
       if constexpr (ACT == ACT_NONE) return launch_one<T, OutT, ACT, 128, 2, 4, 3, 64, 1, 4>(p, st);
-      else return launch_one<T, OutT, ACT, 128, 2, 4, 3, 128, 1, 4>(p, st);
+      else {
+        if (launch_gated_persist<T, OutT, ACT>(p, st) == FLIDE_MOE_OK) return FLIDE_MOE_OK;
+        return launch_one<T, OutT, ACT, 128, 2, 4, 3, 128, 1, 4>(p, st);
+      }
     }
     if (bm == 64) {   // 128-byte stage rows: down in 8 waves, gate/up in two 4-wave workgroups of BN 128
       if constexpr (ACT == ACT_NONE) return launch_one<T, OutT, ACT, 64, 2, 4, 3, 128, 1, 8>(p, st);
