@@ -1022,7 +1022,8 @@ int launch_fp8_resident(GroupArgs& p, hipStream_t st) {
 //     register-streaming kernel (gate/up 180 -> 170 us, down 112 -> 94 us at 64 tokens; fp8 110 ->
 //     95 / 61 -> 52 us)
 // ---------------------------------------------------------------------------------------------------
-// Persistent gated product (float8 or 16-bit): bm 128, BN 256, split roles, staged epilogue
+// Persistent products: bm 128, BN 256, split roles (gated: float8 or 16-bit, staged epilogue; plain:
+// 16-bit weights with float32 outputs)
 // ---------------------------------------------------------------------------------------------------
 // At 4096 tokens the per-tile kernel spends about a third of a float8 gate/up tile's life outside its K
 // loop: the start-up chain (the item's expert, its pairs, the first stages) and the epilogue, while the
@@ -1035,11 +1036,15 @@ int launch_fp8_resident(GroupArgs& p, hipStream_t st) {
 // ends, so its first stages land during this item's last MFMAs and epilogue. The next item's metadata
 // moves only through LDS, written after one stage barrier and read after a later one (see act()).
 // Barriers per item, for every wave: the item's nk stage barriers, then two in the epilogue.
-// The arithmetic is grouped_dma's gated path (K steps, MFMA order, epilogue), so the bits are too.
-// 16-bit weights: 64 K per 128-byte stage row as two 32-wide MFMA steps, no scales.
+// The arithmetic is grouped_dma's (K steps, MFMA order, epilogue), so the bits are too. 16-bit weights:
+// 64 K per 128-byte stage row as two 32-wide MFMA steps, no scales. Plain (down) products: items in
+// grouped_dma's block-major order, the rows' routing weights in place of the activation scales, and
+// the float32 epilogue of 16-byte stores from registers (no staging, no epilogue barriers).
 template <typename T, typename OutT, int ACT>
-__global__ __launch_bounds__(12 * 64, 1) void grouped_gated_persist(GroupArgs p) {
+__global__ __launch_bounds__(12 * 64, 1) void grouped_persist(GroupArgs p) {
   constexpr bool FP8 = std::is_same<T, Fp8Tag>::value;
+  constexpr bool GATED = ACT != ACT_NONE;
+  constexpr int EPB = GATED ? 2 : 0;   // barriers in an item's epilogue
   constexpr int EB = DmaElem<T>::BYTES;
   constexpr int BM = 128, BN = 256, NS = 3, ROWB = 128, NW = 8, NLD = 4, WAVES_M = 2;
   constexpr int CPR = 8, RPI = 8, KS = ROWB / EB;   // K per 128-byte stage row
@@ -1049,17 +1054,19 @@ __global__ __launch_bounds__(12 * 64, 1) void grouped_gated_persist(GroupArgs p)
   static_assert(FM == 4 && FN == 4 && (NS - 1) * L < 64, "2 x 4 waves of 64 x 64, loads in flight fit vmcnt");
   typedef typename OutTraits<OutT>::storage S;
   typedef typename std::conditional<FP8, typename OutRound<OutT>::type, T>::type RT;   // gate/up rounding
-  static_assert(sizeof(S) == 2, "16-bit outputs");
+  static_assert(GATED ? sizeof(S) == 2 : (!FP8 && std::is_same<OutT, float>::value),
+                "gated: 16-bit outputs; plain: 16-bit weights, float32 outputs");
   __shared__ __attribute__((aligned(1024))) char lds0[STAGE];
   __shared__ __attribute__((aligned(1024))) char lds1[STAGE];
   __shared__ __attribute__((aligned(1024))) char lds2[STAGE];
   __shared__ int s_pairs[2][BM];
-  __shared__ float s_ascale[2][BM];
+  __shared__ float s_ascale[2][BM];   // the rows' activation scales (gated float8) or routing weights (plain)
   __shared__ int s_meta[2][4];   // the item's block, column tile and expert
 
   const int tid = threadIdx.x, l = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int K = p.K, half = p.N / 2, nk = K / KS;
+  const int ncols = GATED ? half : p.N;
   // this workgroup's items: XCD x's range of the items in use, every W-th from j
   const int nused = *p.used / BM;
   const long long R = (long long)nused * p.ntn;
@@ -1069,7 +1076,8 @@ __global__ __launch_bounds__(12 * 64, 1) void grouped_gated_persist(GroupArgs p)
   if (n_items == 0) return;
 
   // item -> (block, column tile, expert) in grouped_dma's prefill order (column-tile major inside an
-  // expert), by one wave: expert_run's window loads, issued apart from their use
+  // expert for the gated products, block major for the plain ones), by one wave: expert_run's window
+  // loads, issued apart from their use
   int wlo = 0, whi = 0;
   auto window = [&](long long it) {
     const int blk = (int)(it / p.ntn);
@@ -1087,12 +1095,13 @@ __global__ __launch_bounds__(12 * 64, 1) void grouped_gated_persist(GroupArgs p)
         mh ? blk + __builtin_ctzll(mh) : expert_end_block(p.blocks, blk + 64, e, nused, l));
     const int local = (int)(it - (long long)s0 * p.ntn), nb = s1 - s0;
     if (l == 0) {
-      meta[0] = s0 + local % nb;
-      meta[1] = local / nb;
+      meta[0] = GATED ? s0 + local % nb : s0 + local / p.ntn;
+      meta[1] = GATED ? local / nb : local % p.ntn;
       meta[2] = e;
     }
   };
-  auto scale_of = [&](int pair) {
+  auto scale_of = [&](int pair) {   // the row value the epilogue reads: activation scale or routing weight
+    if constexpr (!GATED) return p.weights && pair < p.n_pairs ? p.weights[pair] : 1.f;
     if constexpr (!FP8) return 1.f;
     return pair < p.n_pairs ? p.a_scale[p.by_token ? pair / p.topk : pair] : 0.f;
   };
@@ -1124,9 +1133,14 @@ __global__ __launch_bounds__(12 * 64, 1) void grouped_gated_persist(GroupArgs p)
 #pragma unroll
       for (int i = 0; i < LB; ++i) {
         const int row = (lw * LB + i) * RPI + l / CPR;
-        int cc = pn * TC + (row < TC ? row : row - TC);
-        if (cc >= half) cc = half - 1;
-        const long long n = row < TC ? cc : cc + half;
+        long long n;
+        if constexpr (GATED) {
+          int cc = pn * TC + (row < TC ? row : row - TC);
+          if (cc >= half) cc = half - 1;
+          n = row < TC ? cc : cc + half;
+        } else {
+          n = min(pn * BN + row, p.N - 1);
+        }
         b_off[buf][i] = (uint32_t)(n * p.sbn * EB + kc);
       }
 #pragma unroll
@@ -1161,8 +1175,8 @@ __global__ __launch_bounds__(12 * 64, 1) void grouped_gated_persist(GroupArgs p)
         if (ks < nk) issue((g + NS - 1) % NS, ks, buf);
         else if (has_next) issue((g + NS - 1) % NS, ks - nk, buf ^ 1);
       }
-      __builtin_amdgcn_s_barrier();   // the epilogue's two barriers
-      __builtin_amdgcn_s_barrier();
+#pragma unroll
+      for (int eb = 0; eb < EPB; ++eb) __builtin_amdgcn_s_barrier();   // the epilogue's barriers
     }
     return;
   }
@@ -1174,10 +1188,12 @@ __global__ __launch_bounds__(12 * 64, 1) void grouped_gated_persist(GroupArgs p)
 #pragma unroll
   for (int jj = 0; jj < 2; ++jj) lane_off[jj] = r * ROWB + ((((jj * 4 + g) % CPR) ^ swz<CPR>(r)) << 4);
   auto a_off = [&](int fm, int jj) { return (wm * WM + fm * 16) * ROWB + lane_off[jj]; };
-  auto b_off = [&](int fn, int jj) {   // gate fragments first, then the matching up fragments
+  auto brow = [&](int fn) {   // gated: gate fragments first, then the matching up fragments
+    if constexpr (!GATED) return wn * WN + fn * 16;
     const int f = fn < FN / 2 ? fn : fn - FN / 2;
-    return A_BYTES + ((fn < FN / 2 ? 0 : TC) + wn * (WN / 2) + f * 16) * ROWB + lane_off[jj];
+    return (fn < FN / 2 ? 0 : TC) + wn * (WN / 2) + f * 16;
   };
+  auto b_off = [&](int fn, int jj) { return A_BYTES + brow(fn) * ROWB + lane_off[jj]; };
   f32x4_t acc[FM][FN];
   int g_stage = 0;
   int pair_next = 0;
@@ -1207,8 +1223,8 @@ __global__ __launch_bounds__(12 * 64, 1) void grouped_gated_persist(GroupArgs p)
       for (int f = 0; f < FN / 2; ++f) {
         const int col = pn * TC + wn * (WN / 2) + f * 16 + r;
         const bool ok = col < half;
-        cs_g[f] = !FP8 ? 1.f : ok ? p.w_scale[e * p.sse + col] : 0.f;
-        cs_u[f] = !FP8 ? 1.f : ok ? p.w_scale[e * p.sse + col + half] : 0.f;
+        cs_g[f] = !FP8 || !GATED ? 1.f : ok ? p.w_scale[e * p.sse + col] : 0.f;
+        cs_u[f] = !FP8 || !GATED ? 1.f : ok ? p.w_scale[e * p.sse + col + half] : 0.f;
       }
     }
     bool m_live[FM];
@@ -1218,9 +1234,9 @@ __global__ __launch_bounds__(12 * 64, 1) void grouped_gated_persist(GroupArgs p)
       m_live[fm] = __builtin_amdgcn_readfirstlane(s_pairs[buf][wm * WM + fm * 16]) < p.n_pairs;
       nlive += m_live[fm] ? 1 : 0;
     }
-    const int colbase0 = pn * TC + wn * (WN / 2);
-    const bool wave_live = colbase0 < half && m_live[0];
-    if (colbase0 >= half) nlive = 0;
+    const int colbase0 = GATED ? pn * TC + wn * (WN / 2) : pn * BN + wn * WN;
+    const bool wave_live = colbase0 < ncols && m_live[0];
+    if (colbase0 >= ncols) nlive = 0;
 #pragma unroll
     for (int fm = 0; fm < FM; ++fm)
 #pragma unroll
@@ -1299,6 +1315,19 @@ __global__ __launch_bounds__(12 * 64, 1) void grouped_gated_persist(GroupArgs p)
     else kloop(std::integral_constant<int, 4>{}, lds0, lds1, lds2);
     const int last = (g_stage + nk - 1) % NS;   // the ring slot of the item's last stage
     g_stage += nk;
+    if constexpr (!GATED) {   // float32 rows, 16 bytes per lane after the quad transpose (store_frag_f32x4)
+      if (wave_live) {   // the ring slot is refilled only after every wave's next stage barrier
+        const float ones[4] = {1.f, 1.f, 1.f, 1.f};
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm) {
+          if (!m_live[fm]) continue;
+#pragma unroll
+          for (int fn = 0; fn < FN; ++fn)
+            store_frag_f32x4(p, s_pairs[buf], s_ascale[buf], wm * WM + fm * 16, colbase0 + fn * 16, acc[fm][fn], ones, 1.f);
+        }
+      }
+      continue;
+    }
 
     // epilogue: the BM x TC activation tile staged in the last stage's slot (the loaders refill it only
     // after the next item's first barrier), then 16-byte row pieces
@@ -1348,17 +1377,21 @@ __global__ __launch_bounds__(12 * 64, 1) void grouped_gated_persist(GroupArgs p)
   }
 }
 
-// the persistent gated product where it applies: 16-bit outputs in 16-byte aligned rows, no routing
-// weights, K a whole number of stages, at least 10 (the next item's metadata needs stages 0-8 of the
-// current one); one workgroup per CU, a multiple of 8
+// the persistent kernel where it applies: gated products with 16-bit outputs in 16-byte aligned rows and
+// no routing weights, plain 16-bit products with float32 outputs in 16-byte aligned rows; K a whole
+// number of stages, at least 10 (the next item's metadata needs stages 0-8 of the current one); one
+// workgroup per CU, a multiple of 8
 template <typename T, typename OutT, int ACT>
-int launch_gated_persist(GroupArgs& p, hipStream_t st) {
+int launch_persist(GroupArgs& p, hipStream_t st) {
   constexpr int KS = 128 / DmaElem<T>::BYTES;
+  constexpr bool FP8 = std::is_same<T, Fp8Tag>::value;
   typedef typename OutTraits<OutT>::storage S;
-  if constexpr (sizeof(S) != 2) {
+  if constexpr (ACT != ACT_NONE ? sizeof(S) != 2 : (FP8 || !std::is_same<OutT, float>::value)) {
     return FLIDE_MOE_ERR_TILE;
   } else {
-    if (p.weights || p.sc % 8 || (uintptr_t)p.out % 16 || p.K % KS || p.K / KS < 10) return FLIDE_MOE_ERR_TILE;
+    if ((ACT != ACT_NONE && p.weights) || p.sc % (16 / sizeof(S)) || (uintptr_t)p.out % 16 || p.K % KS ||
+        p.K / KS < 10)
+      return FLIDE_MOE_ERR_TILE;
     static int cus[64] = {0};
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return FLIDE_MOE_ERR_TILE;
@@ -1368,9 +1401,9 @@ int launch_gated_persist(GroupArgs& p, hipStream_t st) {
         return FLIDE_MOE_ERR_TILE;
       cus[dev] = n / 8 * 8;
     }
-    p.ntn = (p.N / 2 + 127) / 128;
-    p.pack_f32 = 0;
-    grouped_gated_persist<T, OutT, ACT><<<dim3(cus[dev]), dim3(12 * 64), 0, st>>>(p);
+    p.ntn = ACT != ACT_NONE ? (p.N / 2 + 127) / 128 : (p.N + 255) / 256;
+    p.pack_f32 = ACT == ACT_NONE;
+    grouped_persist<T, OutT, ACT><<<dim3(cus[dev]), dim3(12 * 64), 0, st>>>(p);
     return FLIDE_MOE_OK;
   }
 }
@@ -1423,7 +1456,7 @@ int launch_dma(GroupArgs& p, int bm, hipStream_t st) {
         return launch_one<T, OutT, ACT, 128, 2, 4, 2, 128, 2, 4, 128>(p, st);
       }
       else {
-        if (launch_gated_persist<T, OutT, ACT>(p, st) == FLIDE_MOE_OK) return FLIDE_MOE_OK;
+        if (launch_persist<T, OutT, ACT>(p, st) == FLIDE_MOE_OK) return FLIDE_MOE_OK;
         return launch_one<T, OutT, ACT, 128, 2, 4, 3, 128, 1, 4, 256, 4>(p, st);   // + 4 loader waves
       }
     }
@@ -1435,9 +1468,11 @@ int launch_dma(GroupArgs& p, int bm, hipStream_t st) {
     }
     if (bm == 256) return launch_one<T, OutT, ACT, 256, 1, 4, 4, 64, 1, 2>(p, st);
     if (bm == 128) {   // 8 waves of 64 x 64, two per SIMD within one workgroup
-      if constexpr (ACT == ACT_NONE) return launch_one<T, OutT, ACT, 128, 2, 4, 3, 64, 1, 4>(p, st);
-      else {
-        if (launch_gated_persist<T, OutT, ACT>(p, st) == FLIDE_MOE_OK) return FLIDE_MOE_OK;
+      if constexpr (ACT == ACT_NONE) {
+        if (launch_persist<T, OutT, ACT>(p, st) == FLIDE_MOE_OK) return FLIDE_MOE_OK;
+        return launch_one<T, OutT, ACT, 128, 2, 4, 3, 64, 1, 4>(p, st);
+      } else {
+        if (launch_persist<T, OutT, ACT>(p, st) == FLIDE_MOE_OK) return FLIDE_MOE_OK;
         return launch_one<T, OutT, ACT, 128, 2, 4, 3, 128, 1, 4>(p, st);
       }
     }
