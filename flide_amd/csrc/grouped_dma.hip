@@ -597,6 +597,19 @@ __global__ __launch_bounds__((WAVES_M * WAVES_N + NLD) * 64, OCC) void grouped_d
   }
 }
 
+// The current device's CUs, rounded down to a multiple of 8 (0 if unknown).
+int cu_count() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cus[dev] = n / 8 * 8;
+  }
+  return cus[dev];
+}
+
 // Float8 plain (down) products with short rows (K <= 768, the 704-wide down product): the block's
 // activation rows stay resident in LDS and NLD loader waves stream the expert's weight tiles through a
 // ring, continuously over several column tiles. With K this short, the per-tile kernel above spends
@@ -619,7 +632,7 @@ __global__ __launch_bounds__((WAVES_M * WAVES_N + NLD) * 64, OCC) void grouped_d
 // Arithmetic: the same 128-wide K steps, lane mapping, MFMA and epilogue order as grouped_dma, so the
 // output bits are the same.
 template <typename OutT, int NS, int BN, int KT_MAX, int XB, int NLD, bool WIDE, bool AREG = false>
-__global__ __launch_bounds__((8 + NLD) * 64, 1) void grouped_fp8_resident(GroupArgs p, int tpb, int nch) {
+__global__ __launch_bounds__((8 + NLD) * 64, 1) void grouped_fp8_resident(GroupArgs p, int tpb, int nch, int cus) {
   constexpr int BM = 128, ROWB = 128;
   // compute waves: WIDE (16-bit outputs, aligned): 8 x 1 waves of 16 rows x BN columns, each wave owning
   // whole output row segments of the tile; else 2 x 4 waves of 64 x BN / 4
@@ -648,10 +661,33 @@ __global__ __launch_bounds__((8 + NLD) * 64, 1) void grouped_fp8_resident(GroupA
   const int b = blockIdx.x;
   const int j = b >> 3;
   const int widx = ((j / CH) * 8 + (b & 7)) * CH + j % CH;
-  const int pm = widx / nch, c = widx % nch;
-  if (pm >= p.nbm || pm * BM >= *p.used) return;
   const int ntn = (p.N + BN - 1) / BN;
-  const int t0 = c * tpb, nt = min(t0 + tpb, ntn) - t0;
+  int pm, c, t0, nt;
+  if (cus > 0) {
+    // Halves of the column tiles (nch = 2), except that the last m blocks, whose items the grid
+    // dispatches last, are cut in thirds, with m such that the items fill whole rounds of the CUs:
+    // the last round then runs items of 8 tiles instead of 11 (at 4096 tokens 648 items, 2.5 rounds,
+    // become 768)
+    const int nused = *p.used / BM;
+    const int m = max(0, min(nused, (2 * nused + cus - 1) / cus * cus - 2 * nused));
+    const int nh = 2 * (nused - m);   // items of the halved blocks
+    if (widx >= nh + 3 * m) return;
+    const int tpb3 = (ntn + 2) / 3;
+    if (widx < nh) {
+      pm = widx / 2, c = widx % 2;
+      t0 = c * tpb;
+      nt = min(t0 + tpb, ntn) - t0;
+    } else {
+      pm = nused - m + (widx - nh) / 3, c = (widx - nh) % 3;
+      t0 = c * tpb3;
+      nt = min(t0 + tpb3, ntn) - t0;
+    }
+  } else {
+    pm = widx / nch, c = widx % nch;
+    if (pm >= p.nbm || pm * BM >= *p.used) return;
+    t0 = c * tpb;
+    nt = min(t0 + tpb, ntn) - t0;
+  }
   if (nt <= 0) return;
   const int K = p.K, KT = (K + ROWB - 1) / ROWB;
   const int S = nt * KT;
@@ -976,7 +1012,9 @@ int launch_fp8_resident(GroupArgs& p, hipStream_t st) {
   const int tpb = (ntn + nch - 1) / nch;
   nch = (ntn + tpb - 1) / tpb;
   p.ntn = ntn;
-  const int items = p.nbm * nch;
+  // two chunks per block: the last blocks' items may be cut in thirds (see the kernel), up to 3 per block
+  const int cus = nch == 2 ? cu_count() : 0;
+  const int items = p.nbm * (cus > 0 ? 3 : nch);
   const int round = 8 * nch * XB;
   dim3 grid((items + round - 1) / round * round), block((8 + NLD) * 64);
   // 16-bit outputs whose rows take 16-byte stores: the WIDE layout, where each store instruction writes
@@ -987,14 +1025,14 @@ int launch_fp8_resident(GroupArgs& p, hipStream_t st) {
       // K of 641..768 (six k-tiles, as the 704-wide down product) with 16-byte aligned activation rows:
       // the rows in registers and a 7-slot weight ring (its column scales need KT >= 6 slots of lead)
       if ((p.K + 127) / 128 == KT_MAX && p.sa % 16 == 0 && (uintptr_t)p.a % 16 == 0) {
-        grouped_fp8_resident<OutT, 7, BN, KT_MAX, XB, NLD, true, true><<<grid, block, 0, st>>>(p, tpb, nch);
+        grouped_fp8_resident<OutT, 7, BN, KT_MAX, XB, NLD, true, true><<<grid, block, 0, st>>>(p, tpb, nch, cus);
         return FLIDE_MOE_OK;
       }
-      grouped_fp8_resident<OutT, NS, BN, KT_MAX, XB, NLD, true><<<grid, block, 0, st>>>(p, tpb, nch);
+      grouped_fp8_resident<OutT, NS, BN, KT_MAX, XB, NLD, true><<<grid, block, 0, st>>>(p, tpb, nch, cus);
       return FLIDE_MOE_OK;
     }
   }
-  grouped_fp8_resident<OutT, NS, BN, KT_MAX, XB, NLD, false><<<grid, block, 0, st>>>(p, tpb, nch);
+  grouped_fp8_resident<OutT, NS, BN, KT_MAX, XB, NLD, false><<<grid, block, 0, st>>>(p, tpb, nch, cus);
   return FLIDE_MOE_OK;
 }
 
@@ -1392,18 +1430,11 @@ int launch_persist(GroupArgs& p, hipStream_t st) {
     if ((ACT != ACT_NONE && p.weights) || p.sc % (16 / sizeof(S)) || (uintptr_t)p.out % 16 || p.K % KS ||
         p.K / KS < 10)
       return FLIDE_MOE_ERR_TILE;
-    static int cus[64] = {0};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return FLIDE_MOE_ERR_TILE;
-    if (cus[dev] == 0) {
-      int n = 0;
-      if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 8)
-        return FLIDE_MOE_ERR_TILE;
-      cus[dev] = n / 8 * 8;
-    }
+    const int cus = cu_count();
+    if (cus < 8) return FLIDE_MOE_ERR_TILE;
     p.ntn = ACT != ACT_NONE ? (p.N / 2 + 127) / 128 : (p.N + 255) / 256;
     p.pack_f32 = ACT == ACT_NONE;
-    grouped_persist<T, OutT, ACT><<<dim3(cus[dev]), dim3(12 * 64), 0, st>>>(p);
+    grouped_persist<T, OutT, ACT><<<dim3(cus), dim3(12 * 64), 0, st>>>(p);
     return FLIDE_MOE_OK;
   }
 }
