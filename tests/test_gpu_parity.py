@@ -339,6 +339,66 @@ def test_grouped_fp8_plain_out_views(layout):
     assert torch.isnan(rest.float()).all(), "a store landed outside the output view"
 
 
+@pytest.mark.parametrize("shape", ["long_runs", "few_items"])
+@pytest.mark.parametrize("kind", ["bf16_geglu", "f16_swiglu", "fp8_geglu", "bf16_plain_w", "f16_plain"])
+def test_grouped_persistent_edges(kind, shape):
+    """The persistent bm-128 products (one workgroup per CU walking its XCD's items; gated 16-bit and
+    float8 with 16-bit out, plain 16-bit with float32 out) at K of exactly 10 stages, the fewest they
+    take (640 for 16-bit, 1280 for float8), in the two places their work order departs from the bench
+    shapes: two experts holding ~80 blocks each ("long_runs": an expert's run of blocks reaches past
+    the 64-entry window on both sides) and ~16 items for 256 workgroups ("few_items": most workgroups
+    own no item). Output views narrower than their row stride (a partial last column tile); columns
+    outside the view stay untouched."""
+    print(f"grouped persistent {kind} {shape}", flush=True)
+    from flide_amd import _hip
+
+    moe = _moe()
+    fp8, gated = kind.startswith("fp8"), not kind.endswith(("plain", "plain_w"))
+    dt = torch.float16 if kind.startswith("f16") else torch.bfloat16
+    T, E, k = (20000, 2, 1) if shape == "long_runs" else (300, 4, 2)
+    K = 1280 if fp8 else 640
+    cols, width = (196, 200) if gated else (298, 300)
+    N = 2 * cols if gated else cols
+    by_token = gated
+    mul_w = kind.endswith("_w")
+    g = torch.Generator().manual_seed(T + K + len(kind))
+    _, ids = orc.route(torch.randn(T, E, generator=g).numpy(), k)
+    x = torch.randn(T if by_token else T * k, K, generator=g).to(dt)
+    w = (torch.randn(E, N, K, generator=g) * 0.03).to(torch.bfloat16 if fp8 else dt)
+    wts = torch.rand(T * k, generator=g)
+    rows, blocks, used = moe.align(torch.from_numpy(ids).to(DEV), E, 128)
+    al = orc.align(ids, E, 128)
+    if shape == "long_runs":
+        nb = int(np.asarray(al["used"]).reshape(-1)[0]) // 128
+        assert np.bincount(al["blocks"][:nb]).min() > 64, "each expert should hold more than 64 blocks"
+    odt = dt if gated else torch.float32
+    odn = {torch.bfloat16: "bf16", torch.float16: "f16", torch.float32: "fp32"}[odt]
+    buf = torch.full((T * k, width), float("nan"), device=DEV, dtype=odt)
+    out = buf[:, :cols]
+    act = (_hip.ACT_GEGLU if "geglu" in kind else _hip.ACT_SWIGLU) if gated else _hip.ACT_NONE
+    wd = wts.to(DEV) if mul_w else None
+    if fp8:
+        qw, sw = orc.quantize_experts(np32(w))
+        qx, sx = orc.quantize_tokens(np32(x))
+        wq = torch.from_numpy(orc.e4m3fn_encode(qw)).view(torch.float8_e4m3fn).to(DEV)
+        moe.grouped_fp8(x.to(DEV), wq, torch.from_numpy(sw).to(DEV), out, rows, blocks, used, k, by_token, wd,
+                        tile=(128, 128, 4, 2), act=act)
+        a_ref, w_ref = qx * sx, qw * sw[:, :, None]
+    else:
+        moe.grouped(x.to(DEV), w.to(DEV), out, rows, blocks, used, k, by_token, wd, tile=(128, 128, 4, 2), act=act)
+        a_ref, w_ref = np32(x), np32(w)
+    gu = orc.grouped(a_ref, w_ref, al["rows"], al["blocks"], al["used"], T * k, k, by_token,
+                     wts.numpy() if mul_w else None, bm=128, out_dtype=odn)
+    if gated:
+        ref = orc.geglu(gu[:, :cols], gu[:, cols:], odn) if "geglu" in kind else orc.swiglu(gu, cols, odn)
+    else:
+        ref = gu
+    assert not np.isnan(np32(out)).any(), "a valid pair's row was not written"
+    # float32 out: fp32 accumulation against the oracle's float64
+    assert_close(np32(out), ref, REL_BF16 if gated else 1e-5, f"persistent {kind} {shape}")
+    assert torch.isnan(buf[:, cols:].float()).all(), "a store landed outside the output view"
+
+
 def _experts_case(cfg, T=None, pairs_subset=None, fp8=False):
     moe = _moe()
     d = inputs(cfg, 0, T)
