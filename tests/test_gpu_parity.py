@@ -466,6 +466,33 @@ def test_experts_fp8_matches_call_sequence(T, E, H, I, dt):
     assert torch.equal(y, ref), f"{(y != ref).sum().item()} of {y.numel()} values differ"
 
 
+@pytest.mark.parametrize("T,E,H,I,dt", [(2100, 16, 1408, 320, torch.bfloat16), (3000, 24, 2816, 704, torch.float16)])
+def test_experts_matches_call_sequence(T, E, H, I, dt):
+    """The 16-bit experts call at the bm-128 tile (persistent products) against the reference's sequence
+    align -> grouped (gate/up with the activation) -> grouped (down, x weight, float32 rows) on the same
+    tiles: the same bits (moe.py:336-353)."""
+    print(f"experts vs call sequence T={T} E={E} H={H} I={I} {dt}", flush=True)
+    moe = _moe()
+    k = 8
+    g = torch.Generator(device=DEV).manual_seed(T + H)
+    logits = torch.randn(T, E, generator=g, device=DEV)
+    x = torch.randn(T, H, generator=g, device=DEV).to(dt)
+    w_gu = (torch.randn(E, 2 * I, H, generator=g, device=DEV) * 0.02).to(dt)
+    w_d = (torch.randn(E, H, I, generator=g, device=DEV) * 0.02).to(dt)
+    top, ids = moe.route(logits, k)
+    tl = moe.tile(T * k, False)
+    assert tl[0] == 128
+    y = moe.experts(x, {"experts": w_gu, "experts_down": w_d, "inter": I}, top, ids, _gelu_act)
+    rows, blocks, used = moe.align(ids, E, tl[0])
+    act = torch.empty(T * k, I, dtype=dt, device=DEV)
+    moe.grouped(x, w_gu, act, rows, blocks, used, k, True, tile=tl, act=_hip_mod().ACT_GEGLU)
+    ref = torch.full((T * k, H), float("nan"), dtype=torch.float32, device=DEV)
+    moe.grouped(act, w_d, ref, rows, blocks, used, k, False, top.reshape(-1), tile=tl)
+    torch.cuda.synchronize()
+    assert not torch.isnan(ref).any()
+    assert torch.equal(y, ref), f"{(y != ref).sum().item()} of {y.numel()} values differ"
+
+
 def test_experts_cfg3_fp8_subset():
     print("experts cfg3 fp8 T=512", flush=True)
     sub = np.sort(np.random.default_rng(0).choice(512 * 8, 512, replace=False))
@@ -807,11 +834,11 @@ def test_graph_replays_match_eager(fp8, T):
     """The Gemma layer captured once into a HIP graph (fused router_norm -> route -> experts ->
     combine_norm_sandwich), replayed three times on new inputs written between replays by eager work: every
     replay gives the bits of an eager run on the same inputs. 48 tokens run the decode tiles, 2100 tokens
-    (8400 pairs) the bm-128 prefill kernels (for float8 gate/up, the split-role form)."""
+    (8400 pairs) the bm-128 prefill kernels, at H = 1408 the persistent gate/up product."""
     print(f"graph replays fp8={fp8} T={T}", flush=True)
     moe = _moe()
     g = torch.Generator().manual_seed(41)
-    H, E, k, I, eps = 512, 16, 4, 128, 1e-6
+    H, E, k, I, eps = (512 if T < 100 else 1408), 16, 4, 128, 1e-6
     assert T < 100 or moe.tile(T * k, fp8)[0] == 128
     bf = torch.bfloat16
     w = {"experts": (torch.randn(E, 2 * I, H, generator=g) * 0.05).to(bf).to(DEV),
